@@ -1,0 +1,128 @@
+/* strata_hip.h — the C ABI of libstrata_hip.so: strata-mlx's decode-step hot path on MI355X (gfx950).
+ *
+ * Conventions
+ *   - Every pointer is device memory the caller owns (e.g. a torch tensor's data_ptr()), except where noted.
+ *   - `stream` is a hipStream_t (NULL: the default stream). Calls only enqueue work; they return at once.
+ *   - Return 0 on success, a negative status on error (SH_E_*); sh_last_error() gives the calling thread's message.
+ *     No C++ exception crosses the ABI. Shape and pointer errors are found before anything is launched.
+ *   - Blocks are a tensor's GGUF bytes as the file has them; a stack of experts is experts x rows x row_bytes.
+ *   - `tables` is the codebook blob (sh_tables_bytes() bytes, layout in csrc/common.h) for the kinds that read
+ *     a codebook (IQ4_*, IQ3_*, IQ2_*, IQ1_M); it may be NULL for Q2_0 and Q3_K.
+ *   - Expert indices that name no expert (< 0 or >= experts) give zero outputs instead of reading out of bounds.
+ *
+ * Each entry point names the reference interface it replaces (paths relative to the strata-mlx repository).
+ */
+#ifndef STRATA_HIP_H
+#define STRATA_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* block kinds: strata_mlx/blocks.py:36-38 (BLOCK) */
+#define SH_KIND_Q2_0 0
+#define SH_KIND_IQ4_NL 1
+#define SH_KIND_IQ4_XS 2
+#define SH_KIND_IQ3_S 3
+#define SH_KIND_IQ3_XXS 4
+#define SH_KIND_IQ2_S 5
+#define SH_KIND_IQ2_XS 6
+#define SH_KIND_IQ2_XXS 7
+#define SH_KIND_IQ1_M 8
+#define SH_KIND_Q3_K 9
+
+/* activation / output element types */
+#define SH_DTYPE_F32 0
+#define SH_DTYPE_F16 1
+#define SH_DTYPE_BF16 2
+
+/* statuses */
+#define SH_OK 0
+#define SH_E_ARG (-1)
+#define SH_E_SHAPE (-2)
+#define SH_E_KIND (-3)
+#define SH_E_DTYPE (-4)
+#define SH_E_HIP (-5)
+#define SH_E_WORKSPACE (-6)
+#define SH_E_UNSUPPORTED (-7)
+
+int sh_version(void);
+const char* sh_last_error(void);
+/* strata_mlx/blocks.py:36-38 (BLOCK): weights and bytes of a block of `kind` (host pointers). */
+int sh_kind_block(int kind, int* weights_per_block, int* bytes_per_block);
+/* strata_mlx/blocks.py:272-289 (_table): bytes of the codebook blob the kernels read. */
+size_t sh_tables_bytes(void);
+
+/* strata_mlx/blocks.py:397-404 (dequantize) and 261-270 (_DEQUANT): every weight of n_mats (rows x cols)
+ * matrices, out_dtype F32 (exact), F16 or BF16 (one rounding). */
+int sh_dequantize(int kind, const void* blocks, const void* tables, int64_t n_mats, int64_t rows, int64_t cols,
+                  void* out, int out_dtype, void* stream);
+
+/* strata_mlx/blocks.py:407-436 (BlockSwitchLinear.__call__, kernel _MATVEC 196-220):
+ * out[pair, r] = W[idx[pair], r, :] . x[pair / share, :], out in x's dtype. bf16/fp16 activations of Q2_0 and
+ * IQ3_S take the MFMA path, everything else exact float32 weights and sums. Pairs sharing an expert read its
+ * blocks once. `workspace` may be NULL when sh_switch_workspace() is 0. */
+size_t sh_switch_workspace(int kind, int64_t rows, int64_t cols, int64_t pairs, int x_dtype);
+int sh_switch_matvec(int kind, const void* blocks, const void* tables, int64_t experts, int64_t rows, int64_t cols,
+                     const int32_t* idx, int64_t pairs, const void* x, int x_dtype, int64_t share, void* out,
+                     void* workspace, size_t workspace_bytes, void* stream);
+/* the same product with exact float32 weights and sums for every kind and dtype (no MFMA); `expert_ptrs`
+ * (device array of per-pair block pointers) replaces blocks + idx when not NULL. */
+int sh_switch_matvec_generic(int kind, const void* blocks, const void* const* expert_ptrs, const void* tables,
+                             int64_t experts, int64_t rows, int64_t cols, const int32_t* idx, int64_t pairs,
+                             const void* x, int x_dtype, int64_t share, void* out, void* stream);
+
+/* strata_mlx/blocks.py:331-346 (matvec_separate): one expert buffer per pair, `expert_ptrs` a device array of
+ * `pairs` pointers. */
+int sh_matvec_separate(int kind, const void* const* expert_ptrs, const void* tables, int64_t rows, int64_t cols,
+                       int64_t pairs, const void* x, int x_dtype, int64_t share, void* out, void* stream);
+
+/* strata_mlx/blocks.py:351-394 (window_matvec): out[t] = W . x[t], one layer, tokens <= 8. */
+int sh_window_matvec(int kind, const void* blocks, const void* tables, int64_t rows, int64_t cols, const void* x,
+                     int x_dtype, int64_t tokens, void* out, void* stream);
+
+/* strata_mlx/blocks.py:782-798 (matvec_glu, kernel _MATVEC_GLU 225-259): out[pair] = W[idx[pair]] .
+ * swiglu(gate[pair], up[pair]) with the reference's roundings; dtype F32, F16 or BF16 for gate, up and out. */
+int sh_matvec_glu(int kind, const void* blocks, const void* tables, int64_t experts, int64_t rows, int64_t cols,
+                  const int32_t* idx, int64_t pairs, const void* gate, const void* up, int dtype, void* out,
+                  void* stream);
+
+/* Q2_0 table of sums: strata_mlx/blocks.py:650-659 (lookup_table), 662-671 (lookup_table_glu), 674-695
+ * (lookup_matvec), 740-760 (lookup_down_glu). Tables are (n, cols / 2, 16) in `dtype`. */
+int sh_lookup_table(const void* x, int dtype, int64_t n, int64_t cols, void* table, void* stream);
+int sh_lookup_table_glu(const void* gate, const void* up, int dtype, int64_t n, int64_t cols, void* table,
+                        void* stream);
+int sh_lookup_matvec(const void* blocks, int64_t experts, int64_t rows, int64_t cols, const int32_t* idx,
+                     int64_t pairs, const void* table, int dtype, int64_t share, void* out, void* stream);
+int sh_lookup_down_glu(const void* blocks, int64_t experts, int64_t rows, int64_t cols, const int32_t* idx,
+                       int64_t pairs, const void* gate, const void* up, int dtype, void* out, void* stream);
+
+/* strata_mlx/fused.py:357-390 (WindowLinear): fp16/bf16 W (rows x cols) times x (tokens <= 8) -> float32. */
+int sh_router_matvec(const void* w, int w_dtype, int64_t rows, int64_t cols, const void* x, int x_dtype,
+                     int64_t tokens, float* out, void* stream);
+
+/* strata_mlx/fused.py:424-436 (top_k, kernel _TOPK 400-418) and 491 (softmax of the chosen logits):
+ * idx (rows x k) of the k largest, largest first, ties to the lower index; weights (nullable) float32. */
+int sh_top_k(const void* logits, int dtype, int64_t rows, int64_t n, int64_t k, int32_t* idx, float* weights,
+             void* stream);
+
+/* strata_mlx/fused.py:467-481 (moe_combine, kernel _COMBINE 448-462): out = OutT(sum_k y_k w_k) +
+ * OutT(OutT(sigmoid(g)) * s). y (tokens, k, d), w (tokens, k) float32, g (tokens), s (tokens, d). */
+int sh_moe_combine(const void* y, const float* w, const void* g, const void* s, int dtype, int64_t tokens,
+                   int64_t k, int64_t d, void* out, void* stream);
+
+/* strata_mlx/blocks.py:539-563 (tiles_of): pairs of idx (pairs = tokens * k) in tiles of 16 slots of one expert.
+ * tile_expert (sh_tiles_most), token (16 * most), where (pairs); workspace sh_tiles_workspace(experts) bytes. */
+size_t sh_tiles_workspace(int64_t experts);
+int64_t sh_tiles_most(int64_t pairs, int64_t experts);
+int sh_tiles_of(const int32_t* idx, int64_t pairs, int64_t k, int64_t experts, int32_t* tile_expert, int32_t* token,
+                int32_t* where, void* workspace, size_t workspace_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* STRATA_HIP_H */

@@ -1,0 +1,295 @@
+// The router and the MoE block's end: the router's product in float32, its top-k with the routing weights, the
+// combine of the experts' outputs with the shared expert, and the prompt's pairs laid out in tiles of one expert.
+#include <type_traits>
+
+#include "decode.h"
+#include "launch.h"
+
+namespace sh {
+
+// ---- router product: W (E x d, fp16 or bf16) times a window of T <= 8 tokens, float32 sums
+// (strata_mlx/fused.py:334-390). One wave a row; each token's sum taken in the same order whatever the window.
+template <typename WT, typename XT>
+__global__ __launch_bounds__(256) void k_router_matvec(const WT* __restrict__ w, const XT* __restrict__ x, int T,
+                                                       float* __restrict__ out, int rows, int cols) {
+  const int lane = threadIdx.x & 63;
+  const int r = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (r >= rows) return;
+  const WT* row = w + (int64_t)r * cols;
+  float acc[8];
+#pragma unroll
+  for (int t = 0; t < 8; ++t) acc[t] = 0.0f;
+  for (int c = lane; c < cols; c += 64) {
+    float wv = to_f32(row[c]);
+#pragma unroll
+    for (int t = 0; t < 8; ++t)
+      if (t < T) acc[t] = fmaf(wv, to_f32(x[(int64_t)t * cols + c]), acc[t]);
+  }
+#pragma unroll
+  for (int t = 0; t < 8; ++t) {
+    if (t < T) {
+      float v = acc[t];
+      for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+      if (lane == 0) out[(int64_t)t * rows + r] = v;
+    }
+  }
+}
+
+// ---- top-k: the indices of the k largest logits of a row, largest first, ties to the lower index
+// (strata_mlx/fused.py:400-418), and optionally the softmax of the chosen logits (fused.py:491).
+//
+// One wave a row. A logit and its index make one 64-bit key that orders as (value, -index): the largest key is the
+// largest value and, among equal values, the lowest index.
+__device__ __forceinline__ uint64_t topk_key(float v, int i) {
+  uint32_t u = __float_as_uint(v);
+  u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);  // float order as unsigned order
+  return ((uint64_t)u << 32) | (uint32_t)(0x7fffffff - i);
+}
+__device__ __forceinline__ float key_value(uint64_t k) {
+  uint32_t u = (uint32_t)(k >> 32);
+  u = (u & 0x80000000u) ? (u & 0x7fffffffu) : ~u;
+  return __uint_as_float(u);
+}
+__device__ __forceinline__ int key_index(uint64_t k) { return 0x7fffffff - (int)(uint32_t)k; }
+
+__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
+  for (int o = 32; o > 0; o >>= 1) {
+    uint32_t lo = __shfl_xor((uint32_t)v, o), hi = __shfl_xor((uint32_t)(v >> 32), o);
+    uint64_t other = ((uint64_t)hi << 32) | lo;
+    v = other > v ? other : v;
+  }
+  return v;
+}
+
+template <typename LT, int VPL>
+__global__ __launch_bounds__(256) void k_top_k(const LT* __restrict__ logits, int rows, int n, int k,
+                                               int32_t* __restrict__ idx, float* __restrict__ weights) {
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const LT* l = logits + (int64_t)row * n;
+  uint64_t key[VPL];
+#pragma unroll
+  for (int i = 0; i < VPL; ++i) {
+    int j = i * 64 + lane;
+    key[i] = j < n ? topk_key(to_f32(l[j]), j) : 0;  // 0: below every real key
+  }
+  float top = 0.0f, sum = 0.0f, chosen = 0.0f;
+  for (int r = 0; r < k; ++r) {
+    uint64_t best = 0;
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) best = key[i] > best ? key[i] : best;
+    best = wave_max_u64(best);
+    int who = key_index(best);
+    float v = key_value(best);
+    if (r == 0) top = v;
+    float e = expf(v - top);
+    sum += e;
+    if (lane == r) chosen = e;
+    if (lane == 0) idx[(int64_t)row * k + r] = who;
+#pragma unroll
+    for (int i = 0; i < VPL; ++i)
+      if (i * 64 + lane == who) key[i] = 0;
+  }
+  if (weights && lane < k) weights[(int64_t)row * k + lane] = chosen / sum;
+}
+
+// ---- the end of the MoE block (strata_mlx/fused.py:448-481):
+// out = OutT(sum_k y_k w_k) + OutT(OutT(sigmoid(g)) * s), the experts added as 8 rows j taking k = j, j + 8, ...
+// then the rows in order, every product rounded before it is added.
+template <typename XT>
+__global__ __launch_bounds__(256) void k_moe_combine(const XT* __restrict__ y, const float* __restrict__ w,
+                                                     const XT* __restrict__ g, const XT* __restrict__ s,
+                                                     XT* __restrict__ out, int K, int D) {
+#pragma clang fp contract(off)
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  const int t = blockIdx.y;
+  if (i >= D) return;
+  float acc = 0.0f;
+  for (int j = 0; j < 8 && j < K; ++j) {
+    float part = 0.0f;
+    for (int kk = j; kk < K; kk += 8) {
+      float prod = to_f32(y[((int64_t)t * K + kk) * D + i]) * w[(int64_t)t * K + kk];
+      part = prod + part;
+    }
+    acc = j == 0 ? part : part + acc;
+  }
+  XT routed = from_f32<XT>(acc);
+  XT gate = from_f32<XT>(1.0f / (1.0f + expf(-to_f32(g[t]))));
+  XT shared = from_f32<XT>(to_f32(gate) * to_f32(s[(int64_t)t * D + i]));
+  out[(int64_t)t * D + i] = from_f32<XT>(to_f32(routed) + to_f32(shared));
+}
+
+// ---- tiles_of (strata_mlx/blocks.py:539-563): the pairs of a prompt chunk in tiles of 16 slots, each tile one
+// expert's; pairs of an expert keep their order. Two kernels: the count of each expert, then one block an expert
+// (and one more for the tiles no pair fills).
+constexpr int TOKENS_TILE = 16;
+
+__global__ __launch_bounds__(1024) void k_tile_counts(const int32_t* __restrict__ flat, int pairs, int experts,
+                                                      int32_t* __restrict__ counts) {
+  extern __shared__ int32_t c[];
+  for (int e = threadIdx.x; e < experts; e += 1024) c[e] = 0;
+  __syncthreads();
+  for (int p = threadIdx.x; p < pairs; p += 1024) {
+    int e = flat[p];
+    if (e >= 0 && e < experts) atomicAdd(&c[e], 1);
+  }
+  __syncthreads();
+  for (int e = threadIdx.x; e < experts; e += 1024) counts[e] = c[e];
+}
+
+__global__ __launch_bounds__(256) void k_tile_place(const int32_t* __restrict__ flat, int pairs, int k, int experts,
+                                                    const int32_t* __restrict__ counts, int most,
+                                                    int32_t* __restrict__ tile_expert, int32_t* __restrict__ token,
+                                                    int32_t* __restrict__ where) {
+  __shared__ int32_t part[256];
+  __shared__ int32_t wave_n[4];
+  const int e = blockIdx.x;
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  // tiles of the experts before this one, and all tiles (the tail block needs the total)
+  int before = 0, all = 0;
+  for (int j = tid; j < experts; j += 256) {
+    int t = (counts[j] + TOKENS_TILE - 1) / TOKENS_TILE;
+    all += t;
+    if (j < e) before += t;
+  }
+  part[tid] = before;
+  __syncthreads();
+  for (int s = 128; s > 0; s >>= 1) {
+    if (tid < s) part[tid] += part[tid + s];
+    __syncthreads();
+  }
+  before = part[0];
+  __syncthreads();
+  part[tid] = all;
+  __syncthreads();
+  for (int s = 128; s > 0; s >>= 1) {
+    if (tid < s) part[tid] += part[tid + s];
+    __syncthreads();
+  }
+  all = part[0];
+  if (e == experts) {  // the tiles no pair fills: no expert, token 0
+    for (int t = all + tid; t < most; t += 256) {
+      tile_expert[t] = experts;
+      for (int j = 0; j < TOKENS_TILE; ++j) token[t * TOKENS_TILE + j] = 0;
+    }
+    return;
+  }
+  const int count = counts[e], tiles = (count + TOKENS_TILE - 1) / TOKENS_TILE;
+  for (int t = tid; t < tiles; t += 256) tile_expert[before + t] = e;
+  for (int j = count + tid; j < tiles * TOKENS_TILE; j += 256) token[before * TOKENS_TILE + j] = 0;
+  // the expert's pairs in order: a running count over the pairs, 256 at a time
+  int seen = 0;
+  for (int base = 0; base < pairs; base += 256) {
+    int p = base + tid;
+    bool mine = p < pairs && flat[p] == e;
+    uint64_t ballot = __ballot(mine);
+    int rank_in_wave = __popcll(ballot & ((1ull << lane) - 1ull));
+    if (lane == 0) wave_n[wv] = __popcll(ballot);
+    __syncthreads();
+    int offset = seen;
+    for (int w = 0; w < wv; ++w) offset += wave_n[w];
+    if (mine) {
+      int slot = before * TOKENS_TILE + offset + rank_in_wave;
+      token[slot] = p / k;
+      where[p] = slot;
+    }
+    seen += wave_n[0] + wave_n[1] + wave_n[2] + wave_n[3];
+    __syncthreads();
+  }
+}
+
+}  // namespace sh
+
+using namespace sh;
+
+extern "C" {
+
+int sh_router_matvec(const void* w, int w_dtype, int64_t rows, int64_t cols, const void* x, int x_dtype,
+                     int64_t tokens, float* out, void* stream) {
+  if (tokens <= 0 || rows <= 0) return OK;
+  if (tokens > 8) return fail(E_SHAPE, "router_matvec: %lld tokens (a window is at most 8)", (long long)tokens);
+  if (cols <= 0 || cols > (1 << 24)) return fail(E_SHAPE, "router_matvec: %lld columns", (long long)cols);
+  if (!w || !x || !out) return fail(E_ARG, "router_matvec: null pointer");
+  return with_half_dtype(w_dtype, [&](auto* wp) {
+    using WT = std::remove_pointer_t<decltype(wp)>;
+    return with_dtype(x_dtype, [&](auto* xp) {
+      using XT = std::remove_pointer_t<decltype(xp)>;
+      hipLaunchKernelGGL((k_router_matvec<WT, XT>), dim3((unsigned)((rows + 3) / 4)), dim3(256), 0,
+                         (hipStream_t)stream, (const WT*)w, (const XT*)x, (int)tokens, out, (int)rows, (int)cols);
+      return check_launch("router_matvec");
+    });
+  });
+}
+
+int sh_top_k(const void* logits, int dtype, int64_t rows, int64_t n, int64_t k, int32_t* idx, float* weights,
+             void* stream) {
+  if (rows <= 0) return OK;
+  if (n <= 0 || n > 2048) return fail(E_SHAPE, "top_k: rows of %lld logits (at most 2048)", (long long)n);
+  if (k <= 0 || k > n || k > 64) return fail(E_SHAPE, "top_k: k = %lld of %lld (at most 64)", (long long)k, (long long)n);
+  if (!logits || !idx) return fail(E_ARG, "top_k: null pointer");
+  int vpl = (int)((n + 63) / 64);
+  vpl = vpl <= 1 ? 1 : vpl <= 2 ? 2 : vpl <= 4 ? 4 : vpl <= 8 ? 8 : vpl <= 16 ? 16 : 32;
+  return with_dtype(dtype, [&](auto* lp) {
+    using LT = std::remove_pointer_t<decltype(lp)>;
+    dim3 grid((unsigned)((rows + 3) / 4));
+    auto go = [&](auto v) {
+      constexpr int V = decltype(v)::value;
+      hipLaunchKernelGGL((k_top_k<LT, V>), grid, dim3(256), 0, (hipStream_t)stream, (const LT*)logits, (int)rows,
+                         (int)n, (int)k, idx, weights);
+      return check_launch("top_k");
+    };
+    switch (vpl) {
+      case 1: return go(kind_c<1>{});
+      case 2: return go(kind_c<2>{});
+      case 4: return go(kind_c<4>{});
+      case 8: return go(kind_c<8>{});
+      case 16: return go(kind_c<16>{});
+      default: return go(kind_c<32>{});
+    }
+  });
+}
+
+int sh_moe_combine(const void* y, const float* w, const void* g, const void* s, int dtype, int64_t tokens, int64_t k,
+                   int64_t d, void* out, void* stream) {
+  if (tokens <= 0) return OK;
+  if (tokens > 65535 || k <= 0 || d <= 0) return fail(E_SHAPE, "moe_combine: shape (%lld, %lld, %lld)",
+                                                     (long long)tokens, (long long)k, (long long)d);
+  if (!y || !w || !g || !s || !out) return fail(E_ARG, "moe_combine: null pointer");
+  return with_dtype(dtype, [&](auto* tp) {
+    using XT = std::remove_pointer_t<decltype(tp)>;
+    dim3 grid((unsigned)((d + 255) / 256), (unsigned)tokens);
+    hipLaunchKernelGGL((k_moe_combine<XT>), grid, dim3(256), 0, (hipStream_t)stream, (const XT*)y, w, (const XT*)g,
+                       (const XT*)s, (XT*)out, (int)k, (int)d);
+    return check_launch("moe_combine");
+  });
+}
+
+// workspace: experts int32 counts
+size_t sh_tiles_workspace(int64_t experts) { return (size_t)(experts > 0 ? experts : 0) * 4; }
+
+int64_t sh_tiles_most(int64_t pairs, int64_t experts) {
+  return pairs / TOKENS_TILE + (experts < pairs ? experts : pairs);
+}
+
+int sh_tiles_of(const int32_t* flat, int64_t pairs, int64_t k, int64_t experts, int32_t* tile_expert, int32_t* token,
+                int32_t* where, void* workspace, size_t workspace_bytes, void* stream) {
+  if (pairs <= 0) return OK;
+  if (k <= 0 || pairs % k) return fail(E_SHAPE, "tiles_of: %lld pairs in rows of %lld", (long long)pairs, (long long)k);
+  if (experts <= 0 || experts > 16384) return fail(E_SHAPE, "tiles_of: %lld experts (at most 16384)", (long long)experts);
+  if (pairs > (1 << 26)) return fail(E_SHAPE, "tiles_of: %lld pairs", (long long)pairs);
+  if (!flat || !tile_expert || !token || !where) return fail(E_ARG, "tiles_of: null pointer");
+  if (!workspace || workspace_bytes < sh_tiles_workspace(experts))
+    return fail(E_WORKSPACE, "tiles_of: workspace of %zu bytes, %zu needed", workspace_bytes, sh_tiles_workspace(experts));
+  int64_t most = sh_tiles_most(pairs, experts);
+  int32_t* counts = (int32_t*)workspace;
+  hipLaunchKernelGGL(k_tile_counts, dim3(1), dim3(1024), (size_t)experts * 4, (hipStream_t)stream, flat, (int)pairs,
+                     (int)experts, counts);
+  int st = check_launch("tiles_of");
+  if (st) return st;
+  hipLaunchKernelGGL(k_tile_place, dim3((unsigned)experts + 1), dim3(256), 0, (hipStream_t)stream, flat, (int)pairs,
+                     (int)k, (int)experts, counts, (int)most, tile_expert, token, where);
+  return check_launch("tiles_of");
+}
+
+}  // extern "C"

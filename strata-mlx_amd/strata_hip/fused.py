@@ -1,0 +1,100 @@
+"""The router's choice and the MoE block's end — strata_mlx/fused.py's interface (router product, top_k,
+moe_combine, the routed MoE block) over HIP kernels (csrc/route.hip)."""
+
+import torch
+
+from . import _lib
+
+ROUTER_TOPK = True   # fused.py:420
+ROUTER_AS_IS = True  # fused.py:421
+COMBINE_UPTO = 65535  # tokens a combine call takes (the reference stops at 16, what it checked against MLX)
+
+
+class WindowLinear:
+    """A float16 / bfloat16 linear layer without bias whose products come back in float32, reading its weights as
+    they are for a window of up to 8 tokens (strata_mlx/fused.py:357-390). `linear` is anything with a `weight`
+    (rows, cols) tensor; longer inputs go through torch's matmul in float32."""
+
+    upto = 8
+
+    def __init__(self, linear):
+        self.linear = linear
+        self.rows, self.cols = linear.weight.shape
+
+    @property
+    def weight(self) -> torch.Tensor:
+        return self.linear.weight
+
+    def takes(self, x: torch.Tensor) -> bool:
+        return x.numel() // self.cols <= self.upto and self.weight.dtype in (torch.float16, torch.bfloat16)
+
+    def __call__(self, x: torch.Tensor) -> torch.Tensor:
+        tokens = x.numel() // self.cols
+        if not self.takes(x):
+            return (x.reshape(-1, self.cols).float() @ self.weight.float().T).reshape(*x.shape[:-1], self.rows)
+        xs = x.reshape(tokens, self.cols).contiguous()
+        w = self.weight.contiguous()
+        out = torch.empty((tokens, self.rows), dtype=torch.float32, device=x.device)
+        _lib.call("sh_router_matvec", w.data_ptr(), _lib.dtype_code(w.dtype), self.rows, self.cols, xs.data_ptr(),
+                  _lib.dtype_code(xs.dtype), tokens, out.data_ptr(), _lib.stream_of(xs))
+        return out.reshape(*x.shape[:-1], self.rows)
+
+
+def top_k(logits: torch.Tensor, k: int, weights: bool = False):
+    """The indices of the k largest logits (..., N), largest first, ties to the lower index — the order
+    `argpartition(-logits, k - 1)[..., :k]` gives (strata_mlx/fused.py:424-436). int32. With weights=True also
+    the softmax of the chosen logits in float32 (fused.py:491), as a second result."""
+    n = logits.shape[-1]
+    flat = logits.reshape(-1, n).contiguous()
+    rows = flat.shape[0]
+    idx = torch.empty((rows, k), dtype=torch.int32, device=logits.device)
+    w = torch.empty((rows, k), dtype=torch.float32, device=logits.device) if weights else None
+    if rows:
+        _lib.call("sh_top_k", flat.data_ptr(), _lib.dtype_code(flat.dtype), rows, n, k, idx.data_ptr(), _lib.ptr(w),
+                  _lib.stream_of(flat))
+    idx = idx.reshape(*logits.shape[:-1], k)
+    return (idx, w.reshape(*logits.shape[:-1], k)) if weights else idx
+
+
+def moe_combine(y: torch.Tensor, w: torch.Tensor, g: torch.Tensor, s: torch.Tensor) -> torch.Tensor | None:
+    """y (..., K, D), w (..., K) float32, g (..., 1), s (..., D) -> (..., D): sum_k y_k w_k rounded to the
+    activations' type, plus sigmoid(g) * s, in the reference's order and roundings (strata_mlx/fused.py:448-481).
+    None where not taken (w not float32, or more tokens than COMBINE_UPTO)."""
+    *lead, k, d = y.shape
+    rows = y.numel() // (k * d) if k * d else 0
+    if rows > COMBINE_UPTO or w.dtype != torch.float32:
+        return None
+    yc = y.reshape(rows, k, d).contiguous()
+    wc = w.reshape(rows, k).contiguous()
+    gc = g.reshape(rows).to(y.dtype).contiguous()
+    sc = s.reshape(rows, d).to(y.dtype).contiguous()
+    out = torch.empty((rows, d), dtype=y.dtype, device=y.device)
+    if rows:
+        _lib.call("sh_moe_combine", yc.data_ptr(), wc.data_ptr(), gc.data_ptr(), sc.data_ptr(), _lib.dtype_code(y.dtype),
+                  rows, k, d, out.data_ptr(), _lib.stream_of(yc))
+    return out.reshape(*lead, d)
+
+
+class Routed:
+    """The MoE block with the router's choice made by `top_k` and its end by `moe_combine`
+    (strata_mlx/fused.py:484-497, the drop-in for mlx-lm's SparseMoeBlock).
+
+    gate: a WindowLinear (or anything returning float32 logits); switch_mlp: a BlockSwitchGLU; shared_expert: a
+    callable x -> (..., D); shared_expert_gate: a callable x -> (..., 1); top_k: experts a token."""
+
+    def __init__(self, gate, switch_mlp, shared_expert, shared_expert_gate, top_k: int):
+        self.gate, self.switch_mlp = gate, switch_mlp
+        self.shared_expert, self.shared_expert_gate = shared_expert, shared_expert_gate
+        self.top_k = top_k
+
+    def __call__(self, x: torch.Tensor) -> torch.Tensor:
+        gate = self.gate
+        as_is = ROUTER_AS_IS and isinstance(gate, WindowLinear) and gate.takes(x)
+        logits = gate(x if as_is else x.float())
+        idx, w = top_k(logits, self.top_k, weights=True)
+        y = self.switch_mlp(x, idx)
+        g, s = self.shared_expert_gate(x), self.shared_expert(x)
+        out = moe_combine(y, w, g, s) if COMBINE_UPTO else None
+        if out is None:
+            out = (y.float() * w[..., None]).sum(dim=-2).to(x.dtype) + torch.sigmoid(g.float()).to(x.dtype) * s
+        return out

@@ -1,0 +1,172 @@
+"""Block products on the GPU against the oracle: dequantized weights bit for bit, products within the path's
+tolerances (1e-5 of max|want| with float32 activations, 1e-2 with bf16/fp16), for all ten kinds."""
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import rel_err
+from oracle import blocks as OB
+from oracle import route as OR
+from strata_hip import blocks as SB
+from strata_hip import synth
+
+pytestmark = pytest.mark.gpu
+
+KINDS = sorted(SB.BLOCK)
+TORCH = {"float32": torch.float32, "float16": torch.float16, "bfloat16": torch.bfloat16}
+TOL = {"float32": 1e-5, "float16": 1e-2, "bfloat16": 1e-2}
+
+
+def stack(kind, experts, rows, cols, seed, tables):
+    rng = np.random.default_rng(seed)
+    raw = synth.random_blocks(kind, experts * rows, cols, rng)
+    w = OB.dequantize(raw, kind, (experts, rows, cols), tables)
+    return raw, w
+
+
+def act(rng, shape, dtype):
+    """activations already in `dtype`, as (torch CPU tensor, float32 numpy values)"""
+    t = torch.from_numpy(rng.standard_normal(shape).astype(np.float32)).to(TORCH[dtype])
+    return t, t.float().numpy()
+
+
+@pytest.mark.parametrize("kind", KINDS)
+@pytest.mark.parametrize("dtype", ["float32", "bfloat16", "float16"])
+def test_dequantize_is_the_oracle_bit_for_bit(kind, dtype, tables, dev):
+    raw, w = stack(kind, 3, 8, 512, 1, tables)
+    got = SB.dequantize(torch.from_numpy(raw).to(dev), kind, (3, 8, 512), TORCH[dtype]).cpu()
+    want = torch.from_numpy(w).to(TORCH[dtype])  # one rounding of the exact weights
+    assert got.dtype == TORCH[dtype] and got.shape == want.shape
+    assert torch.equal(got.view(torch.int16 if dtype != "float32" else torch.int32),
+                       want.view(torch.int16 if dtype != "float32" else torch.int32))
+
+
+@pytest.mark.parametrize("kind", KINDS)
+@pytest.mark.parametrize("dtype", ["float32", "bfloat16", "float16"])
+@pytest.mark.parametrize("share", [1, 2])
+def test_switch_matvec(kind, dtype, share, tables, dev):
+    E, R, C = 5, 48, 512
+    raw, w = stack(kind, E, R, C, 2, tables)
+    rng = np.random.default_rng(3)
+    idx = np.array([4, 0, 0, 2, 3, 3, 3, 1, 4, 2])  # repeats: tokens share experts
+    x, xv = act(rng, (len(idx) // share, C), dtype)
+    got = SB.switch_matvec(torch.from_numpy(raw).to(dev), kind, (E, R, C), torch.from_numpy(idx).to(dev),
+                           x.to(dev), share)
+    assert got.dtype == TORCH[dtype] and got.shape == (len(idx), R)
+    want = OB.matvec(w, idx, xv, share)
+    assert rel_err(got.float().cpu(), want) <= TOL[dtype]
+
+
+@pytest.mark.parametrize("kind", ["Q2_0", "IQ3_S"])
+@pytest.mark.parametrize("dtype", ["bfloat16", "float16"])
+@pytest.mark.parametrize("pairs", [1, 3, 16, 40, 80, 200])
+def test_mfma_path_against_the_oracle(kind, dtype, pairs, tables, dev):
+    """The MFMA decode path at decode shapes: 2048 columns, pairs grouped by expert (up to 128) or one a block,
+    experts chosen by many tokens (more than a group holds) and by one."""
+    E, R, C = 24, 64, 2048
+    raw, w = stack(kind, E, R, C, 4, tables)
+    rng = np.random.default_rng(pairs)
+    idx = rng.integers(0, E, pairs)
+    if pairs >= 40:
+        idx[: pairs // 3] = 7  # one expert chosen by many tokens
+    x, xv = act(rng, (pairs, C), dtype)
+    got = SB.switch_matvec(torch.from_numpy(raw).to(dev), kind, (E, R, C), torch.from_numpy(idx).to(dev),
+                           x.to(dev), 1)
+    assert rel_err(got.float().cpu(), OB.matvec(w, idx, xv, 1)) <= TOL[dtype]
+
+
+def test_a_pair_naming_no_expert_gets_zeros(tables, dev):
+    E, R, C = 3, 32, 256
+    raw, w = stack("Q2_0", E, R, C, 5, tables)
+    idx = np.array([1, 7, 0, -2])
+    x = torch.randn(4, C).to(torch.bfloat16)
+    got = SB.switch_matvec(torch.from_numpy(raw).to(dev), "Q2_0", (E, R, C), torch.from_numpy(idx).to(dev),
+                           x.to(dev), 1).float().cpu()
+    assert (got[1] == 0).all() and (got[3] == 0).all()
+    assert rel_err(got[[0, 2]], OB.matvec(w, idx[[0, 2]], x.float().numpy()[[0, 2]], 1)) <= 1e-2
+
+
+@pytest.mark.parametrize("kind", KINDS)
+@pytest.mark.parametrize("per", [1, 2])
+def test_block_switch_linear_share_modes(kind, per, tables, dev):
+    """tests/test_blocks.py:22-39: a row to each token (gate/up) and a row to each pair (down)."""
+    E, R, C = 3, 16, 512
+    raw, w = stack(kind, E, R, C, 6, tables)
+    layer = SB.BlockSwitchLinear(torch.from_numpy(raw).to(dev), kind, (E, R, C))
+    idx = np.array([[2, 0], [1, 1], [0, 2], [2, 2], [0, 1]])
+    rng = np.random.default_rng(7)
+    x = rng.standard_normal((5, per, 1, C)).astype(np.float32)
+    got = layer(torch.from_numpy(x).to(dev), torch.from_numpy(idx).to(dev)).cpu().numpy()
+    assert got.shape == (5, 2, 1, R)
+    xs = x[:, 0, 0] if per == 1 else x[:, :, 0]
+    want = np.einsum("tkoi,ti->tko", w[idx], xs) if per == 1 else np.einsum("tkoi,tki->tko", w[idx], xs)
+    assert rel_err(got[:, :, 0], want) <= 1e-5
+
+
+@pytest.mark.parametrize("kind", KINDS)
+@pytest.mark.parametrize("tokens", [1, 3, 8])
+def test_window_matvec(kind, tokens, tables, dev):
+    raw, w = stack(kind, 1, 40, 512, 8, tables)
+    rng = np.random.default_rng(9)
+    x, xv = act(rng, (tokens, 512), "float32")
+    got = SB.window_matvec(torch.from_numpy(raw).to(dev), kind, 40, 512, x.to(dev)).cpu()
+    assert rel_err(got, xv.astype(np.float64) @ w[0].T.astype(np.float64)) <= 1e-5
+    # a token's bits do not depend on the window it is in
+    alone = torch.cat([SB.window_matvec(torch.from_numpy(raw).to(dev), kind, 40, 512, x[t:t + 1].to(dev)).cpu()
+                       for t in range(tokens)])
+    assert torch.equal(alone, got)
+
+
+@pytest.mark.parametrize("kind", ["Q2_0", "IQ4_XS", "IQ1_M"])
+def test_matvec_separate(kind, tables, dev):
+    E, R, C = 4, 24, 512
+    raw, w = stack(kind, E, R, C, 10, tables)
+    per = len(raw) // E
+    experts = [torch.from_numpy(raw[e * per:(e + 1) * per].copy()).to(dev) for e in (2, 0, 3, 3)]
+    rng = np.random.default_rng(11)
+    x, xv = act(rng, (2, C), "float32")
+    got = SB.matvec_separate(experts, kind, R, C, x.to(dev), 2).cpu()
+    assert rel_err(got, OB.matvec(w, np.array([2, 0, 3, 3]), xv, 2)) <= 1e-5
+
+
+@pytest.mark.parametrize("kind", ["Q2_0", "IQ3_S", "IQ2_XS"])
+@pytest.mark.parametrize("dtype", ["bfloat16", "float16", "float32"])
+def test_matvec_glu_takes_swiglu_itself(kind, dtype, tables, dev):
+    E, R, C = 4, 32, 256
+    raw, w = stack(kind, E, R, C, 12, tables)
+    rng = np.random.default_rng(13)
+    idx = np.array([1, 3, 3, 0, 2])
+    g, gv = act(rng, (5, C), dtype)
+    u, uv = act(rng, (5, C), dtype)
+    layer = SB.BlockSwitchLinear(torch.from_numpy(raw).to(dev), kind, (E, R, C))
+    got = SB.matvec_glu(layer, torch.from_numpy(idx).to(dev), g.to(dev), u.to(dev)).float().cpu()
+    h = OR.swiglu(gv, uv, dtype)
+    assert rel_err(got, OB.matvec(w, idx, h, 1)) <= TOL[dtype]
+
+
+@pytest.mark.parametrize("pairs", [1, 10, 30])
+@pytest.mark.parametrize("rows, cols", [(256, 640), (96, 128), (40, 2048)])
+def test_the_glu_table_built_in_down_gives_the_bits_of_its_own_kernel(pairs, rows, cols, tables, dev):
+    """tests/test_blocks.py:215-229."""
+    rng = np.random.default_rng(pairs + rows)
+    raw = synth.random_blocks("Q2_0", 3 * rows, cols, rng, dist="uniform")
+    down = SB.BlockSwitchLinear(torch.from_numpy(raw).to(dev), "Q2_0", (3, rows, cols))
+    idx = torch.from_numpy(rng.integers(0, 3, pairs)).to(dev)
+    gate = torch.from_numpy(rng.standard_normal((pairs, cols)).astype(np.float16)).to(dev)
+    up = torch.from_numpy(rng.standard_normal((pairs, cols)).astype(np.float16)).to(dev)
+    got = SB.lookup_down_glu(down, idx, gate, up)
+    assert got is not None and got.dtype == torch.float16
+    assert torch.equal(got, SB.lookup_matvec(down, idx, SB.lookup_table_glu(gate, up), 1))
+
+
+def test_lookup_matvec_is_the_product(tables, dev):
+    E, R, C = 3, 64, 512
+    raw, w = stack("Q2_0", E, R, C, 14, tables)
+    lin = SB.BlockSwitchLinear(torch.from_numpy(raw).to(dev), "Q2_0", (E, R, C))
+    rng = np.random.default_rng(15)
+    x, xv = act(rng, (2, C), "float16")
+    idx = np.array([0, 2, 1, 1])
+    table = SB.lookup_table(x.to(dev))
+    got = SB.lookup_matvec(lin, torch.from_numpy(idx).to(dev), table, 2).float().cpu()
+    assert rel_err(got, OB.matvec(w, idx, xv, 2)) <= 1e-2
