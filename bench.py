@@ -1,0 +1,249 @@
+"""MoE-layer decode on one MI355X: microseconds a layer and effective HBM GB/s, Q2_0 experts, batch 1-8 tokens.
+
+Workload (synthetic, seeded): d_model 2048, 512 routed experts + 1 shared, expert width 512, SwiGLU, every expert
+weight in GGUF Q2_0 blocks (453 MB a layer); router logits bf16 N(0,1), softmax then top-10 with renormalised
+weights; hidden states bf16 N(0,1). A step is one decode pass through 48 distinct such layers (21.7 GB of expert
+blocks, far beyond the 256 MB Infinity Cache) at each verify width B = 1, 2, 4, 8, as the reference times its
+48-layer chains. Each width's 48 layers are one captured graph on one stream, so layer after layer runs in order.
+
+value = algorithmic bytes of all timed layers / their time, where a layer's bytes are the blocks of the experts its
+tokens actually chose (counted from the routing) plus the shared expert, plus activations in and out:
+(U + 1) * 884,736 + B * 9,216 + 4,096.
+
+roofline: the dominant kernel (gate/up with SwiGLU, two thirds of the expert bytes), its launches timed by HIP
+events around a graph of them alone. cpu_baseline: the numpy oracle's restatement of the reference's dequantize +
+matmul path on the host, one thread, over a bounded sample of the same layers.
+
+    python bench.py [--steps K] [--warmup W] [--layers 48] [--batches 1,2,4,8] [--no-cpu]
+"""
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for p in (os.path.join(ROOT, "strata-mlx_amd"), ROOT):
+    if p not in sys.path:
+        sys.path.insert(0, p)
+
+METRIC = "MoE-layer decode µs + effective HBM GB/s (Q2_0, IQ3_S), batch 1-8 tokens"
+E, D, F, K = 512, 2048, 512, 10
+EXPERT_BYTES = 3 * 294_912  # gate + up + down of one Q2_0 expert
+HBM_PEAK_GBS = 8000.0
+
+
+def layer_bytes(u: int, b: int) -> int:
+    return (u + 1) * EXPERT_BYTES + b * 9_216 + 4_096
+
+
+def gate_up_bytes(u: int, b: int) -> int:
+    # gate + up blocks of the chosen and the shared experts, x in, swiglu(gate, up) out
+    return (u + 1) * 2 * 294_912 + b * D * 2 + (b * K + b) * F * 2
+
+
+def build_layers(n_layers, dev, kind):
+    import torch
+
+    from strata_hip import blocks as SB
+    from strata_hip import fused as SF
+    from strata_hip import synth
+
+    layers, raw = [], []
+    for l in range(n_layers):
+        s = 100 * (l + 1)
+        g = synth.random_blocks_gpu(kind, E * F, D, s + 1, dev)
+        u = synth.random_blocks_gpu(kind, E * F, D, s + 2, dev)
+        d = synth.random_blocks_gpu(kind, E * D, F, s + 3, dev)
+        sg = synth.random_blocks_gpu(kind, F, D, s + 4, dev)
+        su = synth.random_blocks_gpu(kind, F, D, s + 5, dev)
+        sd = synth.random_blocks_gpu(kind, D, F, s + 6, dev)
+        gen = torch.Generator(device=dev)
+        gen.manual_seed(s + 7)
+        wg = (torch.randn(D, device=dev, generator=gen) * 0.02).to(torch.bfloat16)
+        lin = [SB.BlockSwitchLinear(t, kind, shape) for t, shape in
+               ((g, (E, F, D)), (u, (E, F, D)), (d, (E, D, F)), (sg, (1, F, D)), (su, (1, F, D)), (sd, (1, D, F)))]
+        layers.append(SF.MoEDecode(*lin, wg, K))
+        raw.append((g, u, d, sg, su, sd, wg))
+    return layers, raw
+
+
+def cpu_baseline(raw, inputs, kind, seconds, check_outputs):
+    """The oracle's restatement of the reference's CPU path (dequantize the touched experts, numpy matmul in
+    float32, the reference's routing, SwiGLU and combine roundings), one thread, on the host cores."""
+    import numpy as np
+    from threadpoolctl import threadpool_limits
+
+    from oracle import blocks as OB
+    from oracle import route as OR
+
+    def one_layer(lw, logits, x):
+        g, u, d, sg, su, sd, wg = lw
+        idx = OR.top_k(logits, K)
+        w = OR.routing_weights(logits, idx)
+        B = x.shape[0]
+        ys = np.zeros((B, K, D), np.float32)
+        experts = {}
+        for e in np.unique(idx):
+            experts[int(e)] = [OB.dequantize(m[int(e)], kind, shape, {}) for m, shape in ((g, (F, D)), (u, (F, D)), (d, (D, F)))]
+        for t in range(B):
+            for j in range(K):
+                wg_, wu_, wd_ = experts[int(idx[t, j])]
+                h = OR.swiglu(OR.to_bf16(wg_ @ x[t]), OR.to_bf16(wu_ @ x[t]), "bfloat16")
+                ys[t, j] = OR.to_bf16(wd_ @ h)
+        shw = [OB.dequantize(m[0], kind, shape, {}) for m, shape in ((sg, (F, D)), (su, (F, D)), (sd, (D, F)))]
+        s = np.stack([OR.to_bf16(shw[2] @ OR.swiglu(OR.to_bf16(shw[0] @ x[t]), OR.to_bf16(shw[1] @ x[t]), "bfloat16"))
+                      for t in range(B)])
+        gate = OR.to_bf16(x @ wg)
+        return OR.moe_combine(ys, w, gate, s, "bfloat16"), len(np.unique(idx))
+
+    host = {}
+    total_bytes, total_time, layers_done, checks = 0, 0.0, 0, {}
+    with threadpool_limits(limits=1):
+        b_list = sorted(inputs)
+        l = 0
+        while True:
+            for b in b_list:
+                logits_t, x_t, gpu_out = inputs[b][l % len(inputs[b])]
+                if l not in host:
+                    g, u, d, sg, su, sd, wg = raw[l % len(raw)]
+                    host[l] = tuple(t.cpu().numpy().reshape(n, -1) for t, n in
+                                    ((g, E), (u, E), (d, E), (sg, 1), (su, 1), (sd, 1))) + (wg.float().cpu().numpy(),)
+                logits, x = logits_t.float().cpu().numpy(), x_t.float().cpu().numpy()
+                t0 = time.perf_counter()
+                out, n_unique = one_layer(host[l], logits, x)
+                total_time += time.perf_counter() - t0
+                total_bytes += layer_bytes(n_unique, b)
+                layers_done += 1
+                if check_outputs and l == 0 and gpu_out is not None:
+                    got = gpu_out.float().cpu().numpy()
+                    checks[b] = float(np.abs(got - out).max() / max(np.abs(out).max(), 1e-30))
+            l += 1
+            if total_time >= seconds or l >= len(raw):
+                break
+    return total_bytes / total_time / 1e9, total_time, layers_done, l, checks
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--layers", type=int, default=48)
+    ap.add_argument("--batches", default="1,2,4,8")
+    ap.add_argument("--kind", default="Q2_0")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: --gpus {args.gpus}: this path is measured on one GPU (expert parallelism across GPUs is "
+              f"a design, not part of this build); run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+
+    import numpy as np
+    import torch
+
+    import strata_hip
+    from strata_hip import fused as SF
+    from strata_hip import tables as T
+
+    strata_hip.load()
+    T.use(T.synthetic(0))
+    dev = torch.device("cuda:0")
+    batches = [int(b) for b in args.batches.split(",")]
+    t_setup = time.perf_counter()
+    layers, raw = build_layers(args.layers, dev, args.kind)
+    torch.cuda.synchronize()
+    print(f"# {args.layers} layers of {args.kind} experts on the GPU in {time.perf_counter() - t_setup:.1f} s",
+          file=sys.stderr, flush=True)
+
+    per_batch, inputs = {}, {}
+    all_bytes, all_time = 0, 0.0
+    gu_bytes, gu_time, gu_launches = 0, 0.0, 0
+    stream = torch.cuda.Stream()
+    for b in batches:
+        gen = torch.Generator(device=dev)
+        gen.manual_seed(1000 + b)
+        logits = [torch.randn(b, E, device=dev, generator=gen).to(torch.bfloat16) for _ in layers]
+        xs = [torch.randn(b, D, device=dev, generator=gen).to(torch.bfloat16) for _ in layers]
+        outs = [torch.empty(b, D, device=dev, dtype=torch.bfloat16) for _ in layers]
+        uniq = [int(torch.unique(SF.top_k(lg, K)).numel()) for lg in logits]
+        bytes_pass = sum(layer_bytes(u, b) for u in uniq)
+        with torch.cuda.stream(stream):
+            for m, lg, x, o in zip(layers, logits, xs, outs):  # first calls allocate the workspaces
+                m(lg, x, out=o)
+            torch.cuda.synchronize()
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph, stream=stream):
+                for m, lg, x, o in zip(layers, logits, xs, outs):
+                    m(lg, x, out=o)
+            # the dominant kernel alone: every layer routed once, then a graph of the gate/up launches only
+            for m, lg, x, o in zip(layers, logits, xs, outs):
+                m(lg, x, phase=0)
+            gu_graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(gu_graph, stream=stream):
+                for m, lg, x, o in zip(layers, logits, xs, outs):
+                    m(lg, x, phase=1)
+            for _ in range(args.warmup):
+                graph.replay()
+                gu_graph.replay()
+            torch.cuda.synchronize()
+            ev = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
+            ev[0].record(stream)
+            for _ in range(args.steps):
+                graph.replay()
+            ev[1].record(stream)
+            ev[2].record(stream)
+            for _ in range(args.steps):
+                gu_graph.replay()
+            ev[3].record(stream)
+            torch.cuda.synchronize()
+            # leave the outputs of a full pass behind (the gate/up graph rewrote h, not the outputs)
+            graph.replay()
+            torch.cuda.synchronize()
+        ms = ev[0].elapsed_time(ev[1])
+        gu_ms = ev[2].elapsed_time(ev[3])
+        n_layers = args.steps * len(layers)
+        per_batch[b] = {"us_per_layer": round(ms * 1e3 / n_layers, 3),
+                        "GBps": round(bytes_pass * args.steps / (ms * 1e-3) / 1e9, 1),
+                        "unique_experts_mean": round(float(np.mean(uniq)), 2),
+                        "tok_per_s": round(b * args.steps / (ms * 1e-3), 1),
+                        "gate_up_us": round(gu_ms * 1e3 / n_layers, 3)}
+        all_bytes += bytes_pass * args.steps
+        all_time += ms * 1e-3
+        gu_bytes += sum(gate_up_bytes(u, b) for u in uniq) * args.steps
+        gu_time += gu_ms * 1e-3
+        gu_launches += n_layers
+        inputs[b] = list(zip(logits, xs, outs))
+        print(f"# B={b}: {per_batch[b]}", file=sys.stderr, flush=True)
+
+    value = all_bytes / all_time / 1e9
+    achieved = gu_bytes / gu_time / 1e9
+    traffic = None
+    cpu = None
+    if not args.no_cpu:
+        gbs, secs, n_done, n_layers_used, checks = cpu_baseline(raw, inputs, args.kind, args.cpu_seconds, True)
+        cpu = {"value": round(gbs, 4), "unit": "GB/s", "cores": 1, "kind": "port",
+               "sample": f"{n_done} layer decodes (layers 0..{n_layers_used - 1} at B = {args.batches}), "
+                         f"{secs:.1f} s: numpy dequantize of the touched experts + float32 matmul, one thread",
+               "check_vs_gpu_rel_err": {str(k): round(v, 6) for k, v in checks.items()}}
+    line = {
+        "metric": METRIC, "value": round(value, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(all_time * 1e3 / args.steps, 4), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
+        "config": {"workload": "moe_layer_decode", "kind": args.kind, "d_model": D, "experts": E, "shared_experts": 1,
+                   "d_ff": F, "top_k": K, "batches": batches, "layers_per_pass": args.layers,
+                   "step": "one decode pass through the layers at each batch width"},
+        "per_batch": {str(k): v for k, v in per_batch.items()},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic, "kernel": "k_moe_gate_up",
+                     "bytes_per_launch": round(gu_bytes / gu_launches), "launches": gu_launches,
+                     "us_per_launch": round(gu_time * 1e6 / gu_launches, 3)},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line))
+
+
+if __name__ == "__main__":
+    main()

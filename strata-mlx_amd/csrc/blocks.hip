@@ -114,15 +114,6 @@ __global__ __launch_bounds__(256) void k_window_matvec(const uint8_t* __restrict
   }
 }
 
-// silu(g) * u as the reference rounds it: sigmoid in float32 rounded to the activations' type, then g * sigma
-// and * u each rounded to that type (strata_mlx/blocks.py:222-237).
-template <typename XT> __device__ __forceinline__ XT swiglu_one(XT g, XT u) {
-  float gf = to_f32(g);
-  float y = 1.0f / (1.0f + expf(fabsf(gf)));
-  XT sig = from_f32<XT>(gf < 0.0f ? y : 1.0f - y);
-  XT a = from_f32<XT>(gf * to_f32(sig));
-  return from_f32<XT>(to_f32(a) * to_f32(u));
-}
 
 // out[pair, r] = W[idx[pair]] . swiglu(gate[pair], up[pair]); the inner activations live in LDS
 template <int KIND, typename XT>

@@ -25,6 +25,8 @@ __host__ __device__ constexpr int bpb(int k) {
        : k == IQ2_S ? 82 : k == IQ2_XS ? 74 : k == IQ2_XXS ? 66 : k == IQ1_M ? 56 : 110;
 }
 
+__host__ __device__ constexpr int64_t row_bytes_dev(int k, int64_t cols) { return cols / wpb(k) * bpb(k); }
+
 // Codebook blob: every table one kernel may need, at fixed 16-byte aligned offsets. The blob is device memory
 // the caller uploads once; kernels that need a table copy it to LDS.
 constexpr int TAB_KVALUES = 0;       // int8 [16]        IQ4_NL / IQ4_XS values (strata_mlx/gguf.py:34)

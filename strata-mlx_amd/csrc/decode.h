@@ -186,6 +186,16 @@ template <> __device__ __forceinline__ void unpack32<IQ1_M>(const uint8_t* row, 
   }
 }
 
+// silu(g) * u as the reference rounds it: sigmoid in float32 rounded to the activations' type, then g * sigma
+// and * u each rounded to that type (strata_mlx/blocks.py:222-237).
+template <typename XT> __device__ __forceinline__ XT swiglu_one(XT g, XT u) {
+  const float gf = to_f32(g);
+  const float y = 1.0f / (1.0f + expf(fabsf(gf)));
+  const XT sig = from_f32<XT>(gf < 0.0f ? y : 1.0f - y);
+  const XT a = from_f32<XT>(gf * to_f32(sig));
+  return from_f32<XT>(to_f32(a) * to_f32(u));
+}
+
 // Copy the tables KIND reads from the blob in global memory to `lds` (small table at 0, grid at LDS_GRID).
 // Every thread of the block takes part; a barrier must follow before use.
 template <int KIND> __device__ __forceinline__ void stage_tables(uint8_t* lds, const uint8_t* blob) {

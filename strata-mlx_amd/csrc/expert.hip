@@ -1,111 +1,16 @@
 // Expert matvec on MFMA: out[pair, r] = W[idx[pair], r, :] . x[pair / share] for bf16 / fp16 activations, the
 // decode path of strata-mlx's BlockSwitchLinear (strata_mlx/blocks.py:196-220, 407-436) rebuilt for CDNA4.
 //
-// Work: a block of 256 threads takes 16 rows of one expert for the tokens that chose it (pairs sharing an expert
-// are grouped in the block itself, so an expert's blocks are read once for every verify token that chose it).
-// The 16 rows' bytes are staged to LDS with 16-byte loads; the 4 waves split the columns, each decoding its
-// share from LDS straight into MFMA operands:
-//
-//   D[token][row] += x[token][k] * q[k][row]      v_mfma_f32_16x16x32_{bf16,f16}
-//
-// with the weights as the B operand, so a lane's accumulators are for the row it decoded (row = lane % 16) and the
-// block scale it decoded applies to them directly. Tokens sit at M-rows 4 * (t / TPG) + t % TPG, so only TPG of a
-// lane's four accumulators are real and the scale costs TPG fmas a group.
-//
-// Decode without multiplies: a code is ORed into the mantissa of a constant ("magic") — for bf16 0x4300 | c is
-// 128 + c — so a pair of weights is one v_and_or. Codes sitting higher in a byte are masked in place (value
-// 128 + U*c) and their activation staged as x / U (exact: a power of two). The constant offsets are removed by a
-// correction MFMA against a constant operand, chained as the accumulator input:
-//   Q2_0:  q = 128 + U c  (bf16) or 1024 + U c (fp16),  correction -(BASE + U)   ->  sum (c - 1) x
-//   IQ3_S: q = 144 + v    (bf16) or 1040 + v  (fp16),   v = +-grid from a 32 KiB LDS table of signed entries,
-//          correction -144 / -1040                     ->  sum v x
-// Every product is exact in float32; the offsets cost precision only in the float32 accumulation (relative error
-// about 1e-6 of a block's sum for bf16), far inside the 1e-2 bf16 tolerance.
-#include <type_traits>
-
-#include "decode.h"
+// A block of 256 threads takes 16 rows of one expert for the tokens that chose it: pairs sharing an expert are
+// grouped in the block itself (up to 128 pairs), so an expert's blocks are read once for every verify token that
+// chose it. The 16 rows' bytes, the tokens' activations and (IQ3_S) the signed codebook are staged to LDS with every
+// load issued before any store; the 4 waves split the columns and decode straight into MFMA operands (xmv.h).
 #include "launch.h"
+#include "xmv.h"
 
 namespace sh {
 
 constexpr int XMV_GROUPED_UPTO = 128;  // pairs grouped by expert inside each block; beyond, a block is a pair
-
-template <typename MT> struct Magic;
-template <> struct Magic<bf16> {
-  static constexpr uint32_t M2 = 0x43004300u;  // two bf16 128.0
-  static constexpr uint32_t HI = 0x43u;        // high byte of a bf16 128 + b
-  static constexpr float BASE = 128.0f;
-};
-template <> struct Magic<f16> {
-  static constexpr uint32_t M2 = 0x64006400u;  // two fp16 1024.0
-  static constexpr uint32_t HI = 0x64u;
-  static constexpr float BASE = 1024.0f;
-};
-
-template <typename MT> __device__ __forceinline__ f32x4 mfma(u32x4 a, u32x4 b, f32x4 c) {
-  if constexpr (std::is_same_v<MT, bf16>)
-    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c,
-                                                   0, 0, 0);
-  else
-    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0,
-                                                  0, 0);
-}
-
-template <typename MT> __device__ __forceinline__ uint32_t pack2(float lo, float hi) {
-  uint16_t a = __builtin_bit_cast(uint16_t, (MT)lo), b = __builtin_bit_cast(uint16_t, (MT)hi);
-  return (uint32_t)a | ((uint32_t)b << 16);
-}
-
-// ---- Q2_0 (64 weights, 18 bytes: fp16 d, then 16 code bytes, byte i holding weights 4i..4i+3)
-//
-// Lane group g = lane / 16 of the wave decodes code bytes 2g, 2g+1, 8+2g, 9+2g of each block for its row: the
-// dword W = b[2+2g] | b[3+2g] << 8 | b[10+2g] << 16 | b[11+2g] << 24. Block-local weight
-// k = 32h + 8g + 4a + j (h: low/high half of W, a: MFMA a or b, j: code within the byte) goes to slot 2j + h of
-// MFMA a. U_j is the scale of the in-place mask of code j.
-template <typename MT> __device__ __forceinline__ float q2_unit(int j) {
-  if constexpr (std::is_same_v<MT, bf16>) return j == 1 ? 4.0f : j == 2 ? 16.0f : 1.0f;  // bits 6-7 shifted down
-  else return j == 1 ? 4.0f : j == 2 ? 16.0f : j == 3 ? 64.0f : 1.0f;
-}
-
-template <typename MT> __device__ __forceinline__ void q2_decode(uint32_t W, u32x4& fa, u32x4& fb) {
-  constexpr uint32_t M = Magic<MT>::M2;
-  const uint32_t W8 = W >> 8;
-  fa.x = (W & 0x00030003u) | M;
-  fa.y = (W & 0x000C000Cu) | M;
-  fa.z = (W & 0x00300030u) | M;
-  fb.x = (W8 & 0x00030003u) | M;
-  fb.y = (W8 & 0x000C000Cu) | M;
-  fb.z = (W8 & 0x00300030u) | M;
-  if constexpr (std::is_same_v<MT, bf16>) {  // bit 7 of a bf16 half is exponent: code 3 shifted to bits 0-1
-    fa.w = ((W >> 6) & 0x00030003u) | M;
-    fb.w = ((W >> 14) & 0x00030003u) | M;
-  } else {
-    fa.w = (W & 0x00C000C0u) | M;
-    fb.w = (W8 & 0x00C000C0u) | M;
-  }
-}
-
-// the correction operand: slot 2j + h holds -(BASE + U_j)
-template <typename MT> __device__ __forceinline__ u32x4 q2_correction() {
-  u32x4 c;
-  c.x = pack2<MT>(-(Magic<MT>::BASE + q2_unit<MT>(0)), -(Magic<MT>::BASE + q2_unit<MT>(0)));
-  c.y = pack2<MT>(-(Magic<MT>::BASE + q2_unit<MT>(1)), -(Magic<MT>::BASE + q2_unit<MT>(1)));
-  c.z = pack2<MT>(-(Magic<MT>::BASE + q2_unit<MT>(2)), -(Magic<MT>::BASE + q2_unit<MT>(2)));
-  c.w = pack2<MT>(-(Magic<MT>::BASE + q2_unit<MT>(3)), -(Magic<MT>::BASE + q2_unit<MT>(3)));
-  return c;
-}
-
-// where activation k of a Q2_0 block goes in the staged layout: fragment (a, g), slot 2j + h; and its scale 1/U
-__device__ __forceinline__ int q2_stage_pos(int kk, int& j) {
-  int h = kk >> 5, g = (kk >> 3) & 3, a = (kk >> 2) & 1;
-  j = kk & 3;
-  return ((a * 4 + g) * 8) + 2 * j + h;  // in elements within the block's 64
-}
-
-// ---- IQ3_S signed table: entry (grid index | sign nibble << 9) -> four bytes 16 +- grid value
-constexpr int IQ3S_SIGNED_BYTES = 8192 * 4;
-
-// ---- the kernel
 
 struct XmvGroup {
   int chunk, expert, n_tok, zero;
@@ -127,9 +32,10 @@ __global__ __launch_bounds__(256) void k_xmv(const uint8_t* __restrict__ blocks,
 
   __shared__ XmvGroup grp;
   __shared__ int s_e[XMV_GROUPED_UPTO], s_rank[XMV_GROUPED_UPTO], s_chunks[XMV_GROUPED_UPTO];
+  __shared__ const XT* s_xrow[NT];
   __shared__ float s_red[4][64][TPG];
   extern __shared__ u32x4 dyn[];
-  // dynamic LDS: [table][staged x: NT tokens x cols][weights: 16 rows + 16 bytes]
+  // dynamic LDS: [signed table][staged x: NT tokens x cols][weights: 16 rows + 16 bytes]
   uint8_t* tab = (uint8_t*)dyn;
   MT* xs = (MT*)((uint8_t*)dyn + xmv_tab_bytes<KIND>());
   uint8_t* wt = (uint8_t*)xs + (size_t)NT * cols * sizeof(MT);
@@ -194,111 +100,41 @@ __global__ __launch_bounds__(256) void k_xmv(const uint8_t* __restrict__ blocks,
       out[(int64_t)grp.orow[i / rows_here] * rows + row0 + i % rows_here] = from_f32<XT>(0.0f);
     return;
   }
+  if (tid < n_tok) s_xrow[tid] = x + (int64_t)grp.xrow[tid] * cols;
+  __syncthreads();
 
-  // 2. the 16 rows' bytes to LDS, at the same address modulo 16 as in memory
+  // 2. the rows' bytes, the table and the activations to LDS: all loads out before any store
   const uint8_t* src = blocks + (int64_t)grp.expert * expert_bytes + (int64_t)row0 * rbytes;
-  const int64_t nbytes = (int64_t)rows_here * rbytes;
-  const uintptr_t a0 = (uintptr_t)src & ~(uintptr_t)15;
-  const int lead = (int)((uintptr_t)src - a0);
-  const int chunks = (int)((lead + nbytes + 15) >> 4);
-  for (int c = tid; c < chunks; c += 256) {
-    const uint8_t* p = (const uint8_t*)(a0 + 16 * (uintptr_t)c);
-    if (p >= src && p + 16 <= src + nbytes) {
-      ((u32x4*)wt)[c] = *(const u32x4*)p;
-    } else {
-      for (int b = 0; b < 16; ++b)
-        if (p + b >= src && p + b < src + nbytes) wt[16 * c + b] = p[b];
-    }
+  ByteStage<4> wst(wt, src, (int)(rows_here * rbytes), tab, signed_tab, xmv_tab_bytes<KIND>());
+  XStage<KIND, XT, MT, 4> xst(xs, s_xrow, n_tok, cols);
+  wst.load(0, tid, 256);
+  xst.load(0, tid, 256);
+  wst.store(0, tid, 256);
+  xst.store(0, tid, 256);
+  for (int p = 1; p < wst.passes(256); ++p) {
+    wst.load(p, tid, 256);
+    wst.store(p, tid, 256);
   }
-  const uint8_t* wrow0 = wt + lead;
-
-  // 3. the table (IQ3_S) and the tokens' activations in the layout the decode wants
-  if constexpr (KIND == IQ3_S) {
-    for (int i = tid; i < IQ3S_SIGNED_BYTES / 16; i += 256) ((u32x4*)tab)[i] = ((const u32x4*)signed_tab)[i];
-  }
-  for (int i = tid; i < n_tok * cols; i += 256) {
-    int t = i / cols, k = i - t * cols;
-    float v = to_f32(x[(int64_t)grp.xrow[t] * cols + k]);
-    if constexpr (KIND == Q2_0) {
-      int j, blk = k >> 6;
-      int pos = q2_stage_pos(k & 63, j);
-      xs[(size_t)t * cols + blk * 64 + pos] = (MT)(v / q2_unit<MT>(j));
-    } else {
-      xs[(size_t)t * cols + k] = (MT)v;
-    }
+  for (int p = 1; p < xst.passes(256); ++p) {
+    xst.load(p, tid, 256);
+    xst.store(p, tid, 256);
   }
   __syncthreads();
 
-  // 4. this wave's quarter of the columns
-  const int g = lane >> 4, n = lane & 15;
-  const int m = n;  // A operand row this lane supplies
-  const int mt = (m & 3) < TPG ? (m >> 2) * TPG + (m & 3) : NT;  // token of A row m, NT if padding
-  const bool real = mt < n_tok;
-  const uint8_t* wrow = wrow0 + (size_t)n * rbytes;  // this lane's weight row (rows beyond rows_here: stale LDS)
+  // 3. this wave's quarter of the columns
   float acc[TPG];
 #pragma unroll
   for (int i = 0; i < TPG; ++i) acc[i] = 0.0f;
-  const f32x4 zero4 = {0.0f, 0.0f, 0.0f, 0.0f};
-  const u32x4 zfrag = {0u, 0u, 0u, 0u};
+  const int per = cols / scale_group<KIND>() / 4;
+  tile_mac<KIND, MT, TPG>(wt + lead_of(src), (int)rbytes, xs, cols, n_tok, wave * per, (wave + 1) * per,
+                          (const uint32_t*)tab, acc);
 
-  if constexpr (KIND == Q2_0) {
-    const int nblk = cols >> 6, per_wave = nblk >> 2;
-    const u32x4 corr = q2_correction<MT>();
-    const MT* xt = xs + (size_t)(real ? mt : 0) * cols;
-    for (int bi = 0; bi < per_wave; ++bi) {
-      const int blk = wave * per_wave + bi;
-      const uint8_t* b = wrow + blk * 18;
-      const uint32_t W = (uint32_t)*(const uint16_t*)(b + 2 + 2 * g) | ((uint32_t)*(const uint16_t*)(b + 10 + 2 * g) << 16);
-      const float d = half_bits(*(const uint16_t*)b);
-      u32x4 fa, fb;
-      q2_decode<MT>(W, fa, fb);
-      u32x4 xa = real ? *(const u32x4*)(xt + blk * 64 + g * 8) : zfrag;
-      u32x4 xb = real ? *(const u32x4*)(xt + blk * 64 + 32 + g * 8) : zfrag;
-      f32x4 D = mfma<MT>(xa, corr, zero4);
-      D = mfma<MT>(xb, corr, D);
-      D = mfma<MT>(xa, fa, D);
-      D = mfma<MT>(xb, fb, D);
-#pragma unroll
-      for (int i = 0; i < TPG; ++i) acc[i] = fmaf(d, D[i], acc[i]);
-    }
-  } else if constexpr (KIND == IQ3_S) {
-    const int runs = cols >> 5, per_wave = runs >> 2;
-    const float cval = -(Magic<MT>::BASE + 16.0f);
-    const uint32_t c2 = pack2<MT>(cval, cval);
-    const u32x4 corr = {c2, c2, c2, c2};
-    const MT* xt = xs + (size_t)(real ? mt : 0) * cols;
-    const uint32_t* stab = (const uint32_t*)tab;
-    constexpr uint32_t HI = Magic<MT>::HI;
-    const uint32_t hi4 = HI * 0x01010101u;
-    for (int ri = 0; ri < per_wave; ++ri) {
-      const int run = wave * per_wave + ri;
-      const uint8_t* b = wrow + (run >> 3) * 110;
-      const int ib = run & 7;
-      const float db = half_bits(*(const uint16_t*)b) * (float)(1 + 2 * (((uint32_t)b[106 + ib / 2] >> (4 * (ib & 1))) & 15u));
-      const uint32_t q2 = *(const uint16_t*)(b + 2 + 8 * ib + 2 * g);
-      const uint32_t qh = (uint32_t)b[66 + ib] >> (2 * g);
-      const uint32_t sg = b[74 + 4 * ib + g];
-      const uint32_t i0 = (q2 & 0xffu) | ((qh & 1u) << 8) | ((sg & 15u) << 9);
-      const uint32_t i1 = (q2 >> 8) | ((qh & 2u) << 7) | ((sg >> 4) << 9);
-      const uint32_t e0 = stab[i0], e1 = stab[i1];
-      u32x4 fw;
-      fw.x = __builtin_amdgcn_perm(hi4, e0, 0x04010400u);
-      fw.y = __builtin_amdgcn_perm(hi4, e0, 0x04030402u);
-      fw.z = __builtin_amdgcn_perm(hi4, e1, 0x04010400u);
-      fw.w = __builtin_amdgcn_perm(hi4, e1, 0x04030402u);
-      u32x4 xa = real ? *(const u32x4*)(xt + run * 32 + g * 8) : zfrag;
-      f32x4 D = mfma<MT>(xa, corr, zero4);
-      D = mfma<MT>(xa, fw, D);
-#pragma unroll
-      for (int i = 0; i < TPG; ++i) acc[i] = fmaf(db, D[i], acc[i]);
-    }
-  }
-
-  // 5. the waves' column quarters summed, one lane a (row, token)
+  // 4. the waves' column quarters summed, one lane a (row, token)
 #pragma unroll
   for (int i = 0; i < TPG; ++i) s_red[wave][lane][i] = acc[i];
   __syncthreads();
   if (wave == 0) {
+    const int g = lane >> 4, n = lane & 15;
 #pragma unroll
     for (int i = 0; i < TPG; ++i) {
       float total = s_red[0][lane][i] + s_red[1][lane][i] + s_red[2][lane][i] + s_red[3][lane][i];

@@ -57,6 +57,8 @@ inline int check_rows(int kind, int64_t rows, int64_t cols, const char* what) {
 
 inline int64_t row_bytes(int kind, int64_t cols) { return cols / wpb(kind) * bpb(kind); }
 
+inline bool mfma_kind_host(int kind) { return kind == Q2_0 || kind == IQ3_S; }
+
 inline int needs_tables(int kind) { return grid_bytes(kind) > 0 || small_bytes(kind) > 0; }
 
 // lanes that share a row in the generic kernels: a power of two, at most a wave, at most the row's runs

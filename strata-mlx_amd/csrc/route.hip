@@ -4,6 +4,7 @@
 
 #include "decode.h"
 #include "launch.h"
+#include "xmv.h"
 
 namespace sh {
 
@@ -39,7 +40,7 @@ __global__ __launch_bounds__(256) void k_router_matvec(const WT* __restrict__ w,
 // (strata_mlx/fused.py:400-418), and optionally the softmax of the chosen logits (fused.py:491).
 //
 // One wave a row. A logit and its index make one 64-bit key that orders as (value, -index): the largest key is the
-// largest value and, among equal values, the lowest index.
+// largest value and, among equal values, the lowest index. The wave's largest key is found on DPP (xmv.h).
 __device__ __forceinline__ uint64_t topk_key(float v, int i) {
   uint32_t u = __float_as_uint(v);
   u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);  // float order as unsigned order
@@ -51,15 +52,6 @@ __device__ __forceinline__ float key_value(uint64_t k) {
   return __uint_as_float(u);
 }
 __device__ __forceinline__ int key_index(uint64_t k) { return 0x7fffffff - (int)(uint32_t)k; }
-
-__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
-  for (int o = 32; o > 0; o >>= 1) {
-    uint32_t lo = __shfl_xor((uint32_t)v, o), hi = __shfl_xor((uint32_t)(v >> 32), o);
-    uint64_t other = ((uint64_t)hi << 32) | lo;
-    v = other > v ? other : v;
-  }
-  return v;
-}
 
 template <typename LT, int VPL>
 __global__ __launch_bounds__(256) void k_top_k(const LT* __restrict__ logits, int rows, int n, int k,
@@ -74,7 +66,9 @@ __global__ __launch_bounds__(256) void k_top_k(const LT* __restrict__ logits, in
     int j = i * 64 + lane;
     key[i] = j < n ? topk_key(to_f32(l[j]), j) : 0;  // 0: below every real key
   }
-  float top = 0.0f, sum = 0.0f, chosen = 0.0f;
+  float top = 0.0f, sum = 0.0f, chosen[VPL];  // chosen[r / 64] at lane r % 64: exp of the r-th largest
+#pragma unroll
+  for (int i = 0; i < VPL; ++i) chosen[i] = 0.0f;
   for (int r = 0; r < k; ++r) {
     uint64_t best = 0;
 #pragma unroll
@@ -85,13 +79,19 @@ __global__ __launch_bounds__(256) void k_top_k(const LT* __restrict__ logits, in
     if (r == 0) top = v;
     float e = expf(v - top);
     sum += e;
-    if (lane == r) chosen = e;
+#pragma unroll
+    for (int i = 0; i < VPL; ++i)
+      if (r == i * 64 + lane) chosen[i] = e;
     if (lane == 0) idx[(int64_t)row * k + r] = who;
 #pragma unroll
     for (int i = 0; i < VPL; ++i)
       if (i * 64 + lane == who) key[i] = 0;
   }
-  if (weights && lane < k) weights[(int64_t)row * k + lane] = chosen / sum;
+  if (weights) {
+#pragma unroll
+    for (int i = 0; i < VPL; ++i)
+      if (i * 64 + lane < k) weights[(int64_t)row * k + i * 64 + lane] = chosen[i] / sum;
+  }
 }
 
 // ---- the end of the MoE block (strata_mlx/fused.py:448-481):
@@ -226,7 +226,7 @@ int sh_top_k(const void* logits, int dtype, int64_t rows, int64_t n, int64_t k, 
              void* stream) {
   if (rows <= 0) return OK;
   if (n <= 0 || n > 2048) return fail(E_SHAPE, "top_k: rows of %lld logits (at most 2048)", (long long)n);
-  if (k <= 0 || k > n || k > 64) return fail(E_SHAPE, "top_k: k = %lld of %lld (at most 64)", (long long)k, (long long)n);
+  if (k <= 0 || k > n) return fail(E_SHAPE, "top_k: k = %lld of %lld", (long long)k, (long long)n);
   if (!logits || !idx) return fail(E_ARG, "top_k: null pointer");
   int vpl = (int)((n + 63) / 64);
   vpl = vpl <= 1 ? 1 : vpl <= 2 ? 2 : vpl <= 4 ? 4 : vpl <= 8 ? 8 : vpl <= 16 ? 16 : 32;

@@ -4,6 +4,7 @@ moe_combine, the routed MoE block) over HIP kernels (csrc/route.hip)."""
 import torch
 
 from . import _lib
+from . import tables as _tables
 
 ROUTER_TOPK = True   # fused.py:420
 ROUTER_AS_IS = True  # fused.py:421
@@ -98,3 +99,76 @@ class Routed:
         if out is None:
             out = (y.float() * w[..., None]).sum(dim=-2).to(x.dtype) + torch.sigmoid(g.float()).to(x.dtype) * s
         return out
+
+
+class MoEDecode:
+    """One MoE block's decode step for up to 16 tokens in three HIP kernels (csrc/moe.hip): route (top-k, weights,
+    the shared expert's gate), gate/up with SwiGLU, down with the combine — what `Routed.__call__` computes
+    (strata_mlx/fused.py:484-497) with the routed experts through switch_glu's bf16 branch (blocks.py:819-829).
+
+    gate / up / down: BlockSwitchLinear stacks (Q2_0 or IQ3_S); shared_*: BlockSwitchLinear of one expert;
+    shared_gate_w: the shared expert gate's weight (d_model,) in the activation type; k: experts a token."""
+
+    MAX_TOKENS = 16
+
+    def __init__(self, gate, up, down, shared_gate, shared_up, shared_down, shared_gate_w: torch.Tensor, k: int):
+        from .blocks import KIND
+
+        self.gate, self.up, self.down = gate, up, down
+        self.shared = (shared_gate, shared_up, shared_down)
+        self.shared_gate_w = shared_gate_w.contiguous()
+        self.k = k
+        self.experts, self.d_ff, self.d_model = gate.num_experts, gate.output_dims, gate.input_dims
+        if up.kind != gate.kind or any(s.kind != l.kind for s, l in zip(self.shared, (gate, up, down))):
+            raise ValueError("gate and up (and the shared expert's) must be of one kind")
+        self.kinds = (KIND[gate.kind], KIND[down.kind])
+        self._ws = {}
+
+    def takes(self, x: torch.Tensor) -> bool:
+        tokens = x.numel() // self.d_model
+        return (0 < tokens <= self.MAX_TOKENS and tokens * self.k <= 256 and x.dtype in (torch.float16, torch.bfloat16)
+                and self.gate.kind in ("Q2_0", "IQ3_S") and self.down.kind in ("Q2_0", "IQ3_S")
+                and self.experts % 64 == 0 and self.experts <= 2048 and self.d_model % 256 == 0
+                and self.d_ff % 256 == 0)
+
+    def workspace(self, tokens: int, dtype: torch.dtype, device) -> torch.Tensor:
+        key = (tokens, dtype, str(device))
+        if key not in self._ws:
+            n = _lib.load().sh_moe_workspace(tokens, self.k, self.d_model, self.d_ff, _lib.dtype_code(dtype))
+            self._ws[key] = torch.zeros(n, dtype=torch.uint8, device=device)
+        return self._ws[key]
+
+    def __call__(self, logits: torch.Tensor, x: torch.Tensor, want_choice: bool = False, phase: int | None = None,
+                 out: torch.Tensor | None = None):
+        """logits (..., experts) float32 or x's type; x (..., d_model). Returns (..., d_model) in x's type, and the
+        choice (idx int32, weights float32) when want_choice. `phase` (0 route, 1 gate/up, 2 down) launches one of
+        the three kernels alone, into `out` for phase 2 (for timing them one by one, in order)."""
+        lead = x.shape[:-1]
+        xs = x.reshape(-1, self.d_model).contiguous()
+        ls = logits.reshape(-1, self.experts).contiguous()
+        tokens = xs.shape[0]
+        if not self.takes(xs):
+            raise ValueError(f"MoEDecode: {tokens} tokens of {xs.dtype} (at most {self.MAX_TOKENS}, bf16/fp16)")
+        if ls.dtype not in (torch.float32, xs.dtype):
+            raise ValueError(f"MoEDecode: logits of {ls.dtype} with activations of {xs.dtype}")
+        ws = self.workspace(tokens, xs.dtype, xs.device)
+        out = torch.empty_like(xs) if out is None else out
+        idx = torch.empty((tokens, self.k), dtype=torch.int32, device=xs.device) if want_choice else None
+        w = torch.empty((tokens, self.k), dtype=torch.float32, device=xs.device) if want_choice else None
+        needs = self.gate.kind == "IQ3_S" or self.down.kind == "IQ3_S"
+        tabs = _tables.device_blob(xs.device).data_ptr() if needs else None
+        sg, su, sd = self.shared
+        if phase is not None:
+            _lib.call("sh_moe_decode_phase", phase, self.kinds[0], self.kinds[1], self.gate.blocks.data_ptr(),
+                      self.up.blocks.data_ptr(), self.down.blocks.data_ptr(), self.experts, sg.blocks.data_ptr(),
+                      su.blocks.data_ptr(), sd.blocks.data_ptr(), self.shared_gate_w.data_ptr(), tabs, ls.data_ptr(),
+                      _lib.dtype_code(ls.dtype), xs.data_ptr(), _lib.dtype_code(xs.dtype), tokens, self.k,
+                      self.d_model, self.d_ff, out.data_ptr(), ws.data_ptr(), ws.numel(), _lib.stream_of(xs))
+            return out
+        _lib.call("sh_moe_decode", self.kinds[0], self.kinds[1], self.gate.blocks.data_ptr(), self.up.blocks.data_ptr(),
+                  self.down.blocks.data_ptr(), self.experts, sg.blocks.data_ptr(), su.blocks.data_ptr(),
+                  sd.blocks.data_ptr(), self.shared_gate_w.data_ptr(), tabs, ls.data_ptr(), _lib.dtype_code(ls.dtype),
+                  xs.data_ptr(), _lib.dtype_code(xs.dtype), tokens, self.k, self.d_model, self.d_ff, out.data_ptr(),
+                  _lib.ptr(idx), _lib.ptr(w), ws.data_ptr(), ws.numel(), _lib.stream_of(xs))
+        out = out.reshape(*lead, self.d_model)
+        return (out, idx, w) if want_choice else out

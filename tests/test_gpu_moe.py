@@ -1,0 +1,82 @@
+"""One MoE block's decode step (route, gate/up + SwiGLU, down + combine) on the GPU against the oracle: the choice of
+experts bit for bit, the routing weights to float32 rounding, the output within 1e-2 of max|want| (bf16/fp16)."""
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import rel_err
+from oracle import blocks as OB
+from oracle import moe as OM
+from strata_hip import blocks as SB
+from strata_hip import fused as SF
+from strata_hip import synth
+
+pytestmark = pytest.mark.gpu
+
+
+def layer(kind, kind_down, E, D, F, seed, dev, tables):
+    rng = np.random.default_rng(seed)
+    raw = {"gate": synth.random_blocks(kind, E * F, D, rng), "up": synth.random_blocks(kind, E * F, D, rng),
+           "down": synth.random_blocks(kind_down, E * D, F, rng),
+           "sgate": synth.random_blocks(kind, F, D, rng), "sup": synth.random_blocks(kind, F, D, rng),
+           "sdown": synth.random_blocks(kind_down, D, F, rng)}
+    kinds = {"gate": kind, "up": kind, "down": kind_down, "sgate": kind, "sup": kind, "sdown": kind_down}
+    shapes = {"gate": (E, F, D), "up": (E, F, D), "down": (E, D, F), "sgate": (1, F, D), "sup": (1, F, D),
+              "sdown": (1, D, F)}
+    lin = {n: SB.BlockSwitchLinear(torch.from_numpy(raw[n]).to(dev), kinds[n], shapes[n]) for n in raw}
+    w = {n: OB.dequantize(raw[n], kinds[n], shapes[n], tables) for n in raw}
+    return lin, w, rng
+
+
+@pytest.mark.parametrize("kinds", [("Q2_0", "Q2_0"), ("IQ3_S", "IQ3_S"), ("IQ3_S", "Q2_0")])
+@pytest.mark.parametrize("tokens", [1, 2, 4, 8, 16])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_moe_decode_is_the_oracles_block(kinds, tokens, dtype, tables, dev):
+    E, D, F, K = 64, 512, 256, 10
+    lin, w, rng = layer(*kinds, E, D, F, tokens, dev, tables)
+    name = "bfloat16" if dtype == torch.bfloat16 else "float16"
+    x = torch.from_numpy(rng.standard_normal((tokens, D)).astype(np.float32)).to(dtype)
+    logits = torch.from_numpy(rng.standard_normal((tokens, E)).astype(np.float32)).to(dtype)
+    if tokens >= 4:
+        logits[1] = logits[0]  # two tokens with one choice: groups of several tokens
+        logits[3] = logits[0]
+    wg = torch.from_numpy(rng.standard_normal(D).astype(np.float32) * 0.05).to(dtype)
+    moe = SF.MoEDecode(lin["gate"], lin["up"], lin["down"], lin["sgate"], lin["sup"], lin["sdown"], wg.to(dev), K)
+    out, idx, wt = moe(logits.to(dev), x.to(dev), want_choice=True)
+    want, want_idx, want_w = OM.moe_decode(logits.float().numpy(), x.float().numpy(), K,
+                                           (w["gate"], w["up"], w["down"]), (w["sgate"], w["sup"], w["sdown"]),
+                                           wg.float().numpy(), name)
+    np.testing.assert_array_equal(idx.cpu().numpy(), want_idx)
+    np.testing.assert_allclose(wt.cpu().numpy(), want_w, rtol=2e-6, atol=1e-7)
+    assert rel_err(out.float().cpu(), want) <= 1e-2
+
+
+@pytest.mark.parametrize("tokens", [1, 8])
+def test_float32_logits_route_exactly(tokens, tables, dev):
+    """A real router gives float32 logits (strata_mlx/fused.py:357-390): the choice is made on them, unrounded."""
+    E, D, F, K = 128, 256, 256, 10
+    lin, w, rng = layer("Q2_0", "Q2_0", E, D, F, 7, dev, tables)
+    x = torch.from_numpy(rng.standard_normal((tokens, D)).astype(np.float32)).to(torch.bfloat16)
+    logits = torch.from_numpy(rng.standard_normal((tokens, E)).astype(np.float32))
+    logits[:, 5] = logits[:, 9]  # exact ties go to the lower index
+    wg = torch.from_numpy(rng.standard_normal(D).astype(np.float32) * 0.05).to(torch.bfloat16)
+    moe = SF.MoEDecode(lin["gate"], lin["up"], lin["down"], lin["sgate"], lin["sup"], lin["sdown"], wg.to(dev), K)
+    out, idx, wt = moe(logits.to(dev), x.to(dev), want_choice=True)
+    want, want_idx, want_w = OM.moe_decode(logits.numpy(), x.float().numpy(), K, (w["gate"], w["up"], w["down"]),
+                                           (w["sgate"], w["sup"], w["sdown"]), wg.float().numpy(), "bfloat16")
+    np.testing.assert_array_equal(idx.cpu().numpy(), want_idx)
+    assert rel_err(out.float().cpu(), want) <= 1e-2
+
+
+def test_repeated_calls_reuse_the_workspace(tables, dev):
+    """The down kernel's row-tile counters return to zero: call after call gives the same bits."""
+    E, D, F, K = 64, 512, 256, 8
+    lin, w, rng = layer("Q2_0", "Q2_0", E, D, F, 3, dev, tables)
+    wg = torch.zeros(D, dtype=torch.bfloat16, device=dev)
+    moe = SF.MoEDecode(lin["gate"], lin["up"], lin["down"], lin["sgate"], lin["sup"], lin["sdown"], wg, K)
+    x = torch.randn(4, D, device=dev).to(torch.bfloat16)
+    logits = torch.randn(4, E, device=dev).to(torch.bfloat16)
+    first = moe(logits, x)
+    for _ in range(5):
+        assert torch.equal(moe(logits, x), first)
