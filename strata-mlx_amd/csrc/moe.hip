@@ -3,22 +3,33 @@
 // (strata_mlx/blocks.py:819-829) and its end in `moe_combine` (fused.py:448-481):
 //
 //   route     one block: each token's top-k of the router logits (largest first, ties to the lower index), the
-//             softmax of the chosen logits, the shared expert's gate logit x . w_g, and the (token, expert) pairs
-//             grouped by expert (first occurrence order), the shared expert as one more group of all B tokens
-//   gate_up   a block = 16 rows of gate and of up of one group's expert, for the group's tokens; its epilogue
-//             rounds gate and up to the activation type and writes swiglu(gate, up) with mlx-lm's roundings
-//   down      a block = 16 rows of down, a wave a group; y rounded to the activation type; the last block to finish
-//             a row tile (an atomic count) combines: OutT(sum_k y_k w_k) + OutT(OutT(sigmoid(g)) * s)
+//             softmax of the chosen logits, the shared expert's gate logit x . w_g, the (token, expert) pairs grouped
+//             by expert (first occurrence order; the shared expert one more group of all B tokens), and the hidden
+//             states written in the layout gate/up's decode reads
+//   gate_up   a block = 16 rows of gate and of up of one group's expert, for the group's tokens; the epilogue rounds
+//             gate and up to the activation type, takes swiglu with mlx-lm's roundings and writes it in the layout
+//             down's decode reads
+//   down      a block = 16 rows of down of every group, chunks of groups double-buffered in LDS, a wave a group; each
+//             pair's outputs rounded to the activation type stay in LDS for the combine:
+//             OutT(sum_k y_k w_k) + OutT(OutT(sigmoid(g)) * s)
 //
-// Grids are sized by the most groups there could be (B*k + 1); blocks past the groups the route found leave at once,
-// so nothing waits on the host. Expert blocks are read straight from the GGUF stacks (xmv.h).
+// Only weights go through LDS: the activations each kernel multiplies were written by the kernel before in the
+// order its MFMA fragments take them, and are read straight from memory (L2). Grids are sized by the most groups
+// there could be (B*k + 1); blocks past the groups the route found leave at once, so nothing waits on the host.
 #include "launch.h"
 #include "xmv.h"
 
 namespace sh {
 
 constexpr int MOE_MAX_TOKENS = 16;
-constexpr int MOE_MAX_PAIRS = 256;  // tokens * k
+constexpr int MOE_MAX_PAIRS = 160;  // tokens * k
+constexpr int MOE_MAX_D = 8192;     // d_model
+
+// experts a multiple of 64 whose count of 64s is a power of two up to 32 (the route's keys a lane holds)
+inline bool vpl_bad(int64_t experts) {
+  const int64_t v = experts / 64;
+  return experts % 64 || v < 1 || v > 32 || (v & (v - 1));
+}
 
 // the workspace, carved from one caller buffer
 struct MoeWs {
@@ -29,9 +40,8 @@ struct MoeWs {
   int32_t* idx;       // [B][k]
   float* w;           // [B][k]
   float* gsh;         // [B]: the shared expert's gate logit, rounded to the activation type
-  int32_t* counter;   // [D / 16]: blocks of down done with a row tile
-  uint8_t* h;         // [B*k + B][F] activation type
-  uint8_t* y;         // [B*k + B][D] activation type
+  uint8_t* xp;        // [B][D]: the hidden states staged for gate/up's kind (xmv.h stage_index)
+  uint8_t* h;         // [B*k + B][F]: swiglu(gate, up), staged for down's kind
 };
 
 static inline size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
@@ -52,9 +62,8 @@ static size_t moe_carve(MoeWs* ws, uint8_t* base, int64_t B, int64_t k, int64_t 
   w.idx = (int32_t*)take(4 * B * k);
   w.w = (float*)take(4 * B * k);
   w.gsh = (float*)take(4 * B);
-  w.counter = (int32_t*)take(4 * (D / 16));
+  w.xp = take((size_t)B * D * es);
   w.h = take((size_t)P * F * es);
-  w.y = take((size_t)P * D * es);
   if (ws) *ws = w;
   return off;
 }
@@ -92,7 +101,7 @@ template <> struct RouteKey<float> {
   __device__ static __forceinline__ uint64_t wave_max(uint64_t k) { return wave_max_u64(k); }
 };
 
-template <typename XT, typename LT>
+template <int KIND, typename XT, typename LT, int VPL>
 __global__ __launch_bounds__(256) void k_moe_route(const LT* __restrict__ logits, const XT* __restrict__ x,
                                                    const XT* __restrict__ wg, int B, int E, int K, int D, MoeWs ws) {
   using RK = RouteKey<LT>;
@@ -100,19 +109,27 @@ __global__ __launch_bounds__(256) void k_moe_route(const LT* __restrict__ logits
   __shared__ int s_idx[MOE_MAX_PAIRS];
   __shared__ int s_first[MOE_MAX_PAIRS], s_gid[MOE_MAX_PAIRS], s_rank[MOE_MAX_PAIRS];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int vpl = E >> 6;  // E a multiple of 64, at most 2048
-  for (int i = tid; i < D / 16; i += 256) ws.counter[i] = 0;
 
   for (int t = wave; t < B; t += 4) {
-    key_t key[32];
+    // every load of the token first: its logits, its hidden state and the shared gate's weights (16-byte vectors)
+    key_t key[VPL];
 #pragma unroll
-    for (int i = 0; i < 32; ++i) key[i] = i < vpl ? RK::make(logits[(int64_t)t * E + i * 64 + lane], i * 64 + lane) : 0;
+    for (int i = 0; i < VPL; ++i) key[i] = RK::make(logits[(int64_t)t * E + i * 64 + lane], i * 64 + lane);
+    u32x4 xv[MOE_MAX_D / 512], wv[MOE_MAX_D / 512];
+#pragma unroll
+    for (int j = 0; j < MOE_MAX_D / 512; ++j) {
+      const int c8 = lane + 64 * j;
+      if (c8 < D / 8) {
+        xv[j] = *(const u32x4*)(x + (int64_t)t * D + 8 * c8);
+        wv[j] = *(const u32x4*)(wg + 8 * c8);
+      }
+    }
     float top = 0.0f, sum = 0.0f, my_e = 0.0f;
     int my_idx = 0;
     for (int r = 0; r < K; ++r) {
-      key_t best = 0;
+      key_t best = key[0];
 #pragma unroll
-      for (int i = 0; i < 32; ++i) best = key[i] > best ? key[i] : best;
+      for (int i = 1; i < VPL; ++i) best = key[i] > best ? key[i] : best;
       best = RK::wave_max(best);  // the same in every lane
       const int who = RK::index(best);
       const float v = RK::value(best);
@@ -125,16 +142,32 @@ __global__ __launch_bounds__(256) void k_moe_route(const LT* __restrict__ logits
         s_idx[t * K + r] = who;
       }
 #pragma unroll
-      for (int i = 0; i < 32; ++i)
+      for (int i = 0; i < VPL; ++i)
         if (key[i] == best) key[i] = 0;
     }
     if (lane < K) {
       ws.w[t * K + lane] = my_e / sum;
       ws.idx[t * K + lane] = my_idx;
     }
-    // the shared expert's gate logit, rounded to the activation type (a Linear(d, 1) in mlx-lm)
+    // the shared expert's gate logit, rounded to the activation type (a Linear(d, 1) in mlx-lm); and the hidden
+    // state in the order gate/up's MFMA fragments take it
     float acc = 0.0f;
-    for (int c = lane; c < D; c += 64) acc = fmaf(to_f32(x[(int64_t)t * D + c]), to_f32(wg[c]), acc);
+    XT* xp = (XT*)ws.xp + (int64_t)t * D;
+#pragma unroll
+    for (int j = 0; j < MOE_MAX_D / 512; ++j) {
+      const int c8 = lane + 64 * j;
+      if (c8 < D / 8) {
+        const XT* a = (const XT*)&xv[j];
+        const XT* b = (const XT*)&wv[j];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          acc = fmaf(to_f32(a[e]), to_f32(b[e]), acc);
+          float scale;
+          const int at = stage_index<KIND, XT>(8 * c8 + e, scale);
+          xp[at] = from_f32<XT>(to_f32(a[e]) * scale);
+        }
+      }
+    }
     acc = wave_sum(acc);
     if (lane == 0) ws.gsh[t] = to_f32(from_f32<XT>(acc));
   }
@@ -163,13 +196,12 @@ __global__ __launch_bounds__(256) void k_moe_route(const LT* __restrict__ logits
   if (tid < P) {
     const int gid = s_gid[s_first[tid]];
     ws.g_pair[gid * 16 + s_rank[tid]] = tid;
-    if (s_rank[tid] == 0) ws.g_expert[gid] = s_idx[tid];
-  }
-  __syncthreads();
-  if (tid < P && s_first[tid] == tid) {
-    int count = 0;
-    for (int q = 0; q < P; ++q) count += s_first[q] == tid;
-    ws.g_ntok[s_gid[tid]] = count;
+    if (s_rank[tid] == 0) {
+      int count = 1;
+      for (int q = tid + 1; q < P; ++q) count += s_first[q] == tid;
+      ws.g_expert[gid] = s_idx[tid];
+      ws.g_ntok[gid] = count;
+    }
   }
   if (tid == 0) {
     int groups = 0;
@@ -181,199 +213,248 @@ __global__ __launch_bounds__(256) void k_moe_route(const LT* __restrict__ logits
   }
 }
 
-// ---- gate and up, SwiGLU in the epilogue
-
-
 template <int KIND> constexpr int moe_tab_bytes() { return KIND == IQ3_S ? IQ3S_SIGNED_BYTES : 0; }
 
-template <int KIND, typename XT, int TPG>
+// ---- gate and up, SwiGLU in the epilogue
+
+template <int KIND, int KIND_DOWN, typename XT, int TPG>
 __global__ __launch_bounds__(256) void k_moe_gate_up(const uint8_t* __restrict__ gate, const uint8_t* __restrict__ up,
                                                      const uint8_t* __restrict__ sh_gate, const uint8_t* __restrict__ sh_up,
-                                                     int E, int K, int B, int D, int F, const XT* __restrict__ x,
+                                                     int E, int K, int B, int D, int F,
                                                      const uint8_t* __restrict__ signed_tab, MoeWs ws) {
-  constexpr int NT = 4 * TPG;
   using MT = XT;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int row0 = blockIdx.x * 16, gy = blockIdx.y;
-  __shared__ int s_n, s_e, s_pair[NT];
-  __shared__ const XT* s_xrow[NT];
+  __shared__ int s_groups, s_n, s_e, s_pair[16];
   __shared__ float s_red[2][4][64][TPG];
   extern __shared__ u32x4 dyn[];
   uint8_t* tab = (uint8_t*)dyn;
-  MT* xs = (MT*)(tab + moe_tab_bytes<KIND>());
   const int64_t rb = row_bytes_dev(KIND, D);
-  uint8_t* wg = (uint8_t*)(xs + NT * D);
+  uint8_t* wg = tab + moe_tab_bytes<KIND>();
   uint8_t* wu = wg + 16 * rb + 16;
-  if (tid == 0) {
-    const int groups = *ws.n_groups;
-    s_n = gy < groups ? ws.g_ntok[gy] : 0;
-    s_e = gy < groups ? ws.g_expert[gy] : 0;
-  }
+  // the group, in one trip: every field read by a thread of its own (entries past the groups are unused)
+  if (tid == 0) s_groups = *ws.n_groups;
+  if (tid == 1) s_e = ws.g_expert[gy];
+  if (tid == 2) s_n = ws.g_ntok[gy];
+  if (tid >= 16 && tid < 32) s_pair[tid - 16] = ws.g_pair[gy * 16 + tid - 16];
   __syncthreads();
+  if (gy >= s_groups) return;
   const int n_tok = s_n, e = s_e;
-  if (n_tok == 0) return;
-  if (tid < n_tok) {
-    const int p = ws.g_pair[gy * 16 + tid];
-    s_pair[tid] = p;
-    s_xrow[tid] = x + (int64_t)(p < B * K ? p / K : p - B * K) * D;
-  }
-  __syncthreads();
   const int64_t ebytes = (int64_t)F * rb;
   const uint8_t* g_src = (e == E ? sh_gate : gate + (int64_t)e * ebytes) + (int64_t)row0 * rb;
   const uint8_t* u_src = (e == E ? sh_up : up + (int64_t)e * ebytes) + (int64_t)row0 * rb;
-  ByteStage<4> wst(wg, g_src, (int)(16 * rb), wu, u_src, (int)(16 * rb));
-  XStage<KIND, XT, MT, 4> xst(xs, s_xrow, n_tok, D);
-  wst.load(0, tid, 256);
-  xst.load(0, tid, 256);
-  wst.store(0, tid, 256);
-  xst.store(0, tid, 256);
-  for (int p = 1; p < wst.passes(256); ++p) {
+  ByteStage<8> wst(wg, g_src, (int)(16 * rb), wu, u_src, (int)(16 * rb));
+  for (int p = 0; p < wst.passes(256); ++p) {
     wst.load(p, tid, 256);
     wst.store(p, tid, 256);
   }
-  for (int p = 1; p < xst.passes(256); ++p) {
-    xst.load(p, tid, 256);
-    xst.store(p, tid, 256);
-  }
   if constexpr (KIND == IQ3_S) {
-    ByteStage<4> tst(tab, signed_tab, IQ3S_SIGNED_BYTES, nullptr, nullptr, 0);
+    ByteStage<8> tst(tab, signed_tab, IQ3S_SIGNED_BYTES, nullptr, nullptr, 0);
     for (int p = 0; p < tst.passes(256); ++p) {
       tst.load(p, tid, 256);
       tst.store(p, tid, 256);
     }
   }
   __syncthreads();
-  float ag[TPG], au[TPG];
+  // this wave's quarter of the columns, the A fragments straight from the staged hidden states
+  const int mt = lane_token<TPG>();
+  const bool real = mt < n_tok;
+  const int p = s_pair[real ? mt : 0];
+  const MT* xg = (const MT*)ws.xp + (int64_t)(p < B * K ? p / K : p - B * K) * D;
+  float acc[2][TPG];
 #pragma unroll
-  for (int i = 0; i < TPG; ++i) ag[i] = au[i] = 0.0f;
+  for (int i = 0; i < TPG; ++i) acc[0][i] = acc[1][i] = 0.0f;
+  const uint8_t* tiles[2] = {wg + lead_of(g_src), wu + lead_of(u_src)};
   const int per = D / scale_group<KIND>() / 4;
-  tile_mac<KIND, MT, TPG>(wg + lead_of(g_src), (int)rb, xs, D, n_tok, wave * per, (wave + 1) * per, (const uint32_t*)tab, ag);
-  tile_mac<KIND, MT, TPG>(wu + lead_of(u_src), (int)rb, xs, D, n_tok, wave * per, (wave + 1) * per, (const uint32_t*)tab, au);
+  tile_mac_global<KIND, MT, TPG, frag_chunk<KIND>(), 2>(tiles, (int)rb, xg, real, wave * per, (wave + 1) * per,
+                                                         (const uint32_t*)tab, acc);
 #pragma unroll
   for (int i = 0; i < TPG; ++i) {
-    s_red[0][wave][lane][i] = ag[i];
-    s_red[1][wave][lane][i] = au[i];
+    s_red[0][wave][lane][i] = acc[0][i];
+    s_red[1][wave][lane][i] = acc[1][i];
   }
   __syncthreads();
   if (wave == 0) {
     const int g = lane >> 4, n = lane & 15;
+    float scale;
+    const int at = stage_index<KIND_DOWN, XT>(row0 + n, scale);
 #pragma unroll
     for (int i = 0; i < TPG; ++i) {
       const int t = g * TPG + i;
       if (t < n_tok) {
         const XT gv = from_f32<XT>(s_red[0][0][lane][i] + s_red[0][1][lane][i] + s_red[0][2][lane][i] + s_red[0][3][lane][i]);
         const XT uv = from_f32<XT>(s_red[1][0][lane][i] + s_red[1][1][lane][i] + s_red[1][2][lane][i] + s_red[1][3][lane][i]);
-        ((XT*)ws.h)[(int64_t)s_pair[t] * F + row0 + n] = swiglu_one(gv, uv);
+        ((XT*)ws.h)[(int64_t)s_pair[t] * F + at] = from_f32<XT>(to_f32(swiglu_one(gv, uv)) * scale);
       }
     }
   }
 }
 
-// ---- down, a wave a group, and the combine by the last block of a row tile
+// ---- down and the combine: a block is 16 output rows of every group's expert
+//
+// The groups go through in chunks of DOWN_CHUNK_G, their weight slices double-buffered in LDS: the next chunk's loads
+// are in flight while this chunk multiplies. A wave takes every fourth group of a chunk; each pair's 16 outputs,
+// rounded to the activation type, stay in LDS for the combine at the end.
 
-constexpr int DOWN_GROUPS = 4;
+constexpr int DOWN_CHUNK_G = 16;
+
+// DOWN_CHUNK_G byte ranges of n bytes (16 rows of an expert) from their own sources to LDS slots of `slot` bytes
+// (alignment kept modulo 16, edge chunks byte by byte): 16 threads a range, a pass of U chunks each.
+template <int U> struct SliceStage {
+  const uint8_t* const* src;
+  uint8_t* dst;
+  int n, nr, slot;
+  u32x4 v[U];
+  bool full[U];
+
+  __device__ __forceinline__ SliceStage(uint8_t* dst_, const uint8_t* const* src_, int nr_, int n_, int slot_)
+      : src(src_), dst(dst_), n(n_), nr(nr_), slot(slot_) {}
+  __device__ __forceinline__ int chunks() const { return (15 + n + 15) >> 4; }
+  __device__ __forceinline__ int passes() const { return (chunks() + 16 * U - 1) / (16 * U); }
+  __device__ __forceinline__ void load(int pass, int tid) {
+    const int r = tid >> 4, j = tid & 15;
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int cc = (pass * U + u) * 16 + j;
+      full[u] = false;
+      if (r < nr && cc < chunks()) {
+        const uint8_t* s = src[r];
+        const uint8_t* p = (const uint8_t*)(((uintptr_t)s & ~(uintptr_t)15) + 16 * (uintptr_t)cc);
+        if (p >= s && p + 16 <= s + n) {
+          v[u] = *(const u32x4*)p;
+          full[u] = true;
+        }
+      }
+    }
+  }
+  __device__ __forceinline__ void store(int pass, int tid) {
+    const int r = tid >> 4, j = tid & 15;
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int cc = (pass * U + u) * 16 + j;
+      if (r >= nr || cc >= chunks()) continue;
+      const uint8_t* s = src[r];
+      const uint8_t* p = (const uint8_t*)(((uintptr_t)s & ~(uintptr_t)15) + 16 * (uintptr_t)cc);
+      uint8_t* d = dst + r * slot + 16 * cc;
+      if (full[u]) {
+        *(u32x4*)d = v[u];
+      } else {
+        for (int b = 0; b < 16; ++b)
+          if (p + b >= s && p + b < s + n) d[b] = p[b];
+      }
+    }
+  }
+};
 
 template <int KIND, typename XT, int TPG>
 __global__ __launch_bounds__(256) void k_moe_down(const uint8_t* __restrict__ down, const uint8_t* __restrict__ sh_down,
                                                   int E, int K, int B, int D, int F,
                                                   const uint8_t* __restrict__ signed_tab, MoeWs ws, XT* __restrict__ out) {
 #pragma clang fp contract(off)
-  constexpr int NT = 4 * TPG;
   using MT = XT;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int row0 = blockIdx.x * 16, by = blockIdx.y;
-  __shared__ int s_groups, s_n[DOWN_GROUPS], s_e[DOWN_GROUPS], s_pair[DOWN_GROUPS][NT], s_last;
-  __shared__ const XT* s_xrow[DOWN_GROUPS][NT];
+  const int row0 = blockIdx.x * 16;
+  const int P = B * K, G = P + 1;
+  __shared__ int s_groups, s_e[MOE_MAX_PAIRS + 1], s_n[MOE_MAX_PAIRS + 1], s_pair[MOE_MAX_PAIRS + 1][16];
+  __shared__ float s_w[MOE_MAX_PAIRS], s_gsh[MOE_MAX_TOKENS];
+  __shared__ float s_y[MOE_MAX_PAIRS + MOE_MAX_TOKENS][16];
+  __shared__ const uint8_t* s_src[2][DOWN_CHUNK_G];
   extern __shared__ u32x4 dyn[];
   uint8_t* tab = (uint8_t*)dyn;
   const int64_t rb = row_bytes_dev(KIND, F);
-  const size_t wave_bytes = (size_t)NT * F * sizeof(MT) + ((16 * rb + 16 + 15) & ~(int64_t)15);
-  uint8_t* mine = tab + moe_tab_bytes<KIND>() + wave * wave_bytes;
-  MT* xs = (MT*)mine;
-  uint8_t* wt = mine + (size_t)NT * F * sizeof(MT);
+  const int slot = (int)(((15 + 16 * rb + 15) >> 4) << 4);
+  uint8_t* buf[2] = {tab + moe_tab_bytes<KIND>(), tab + moe_tab_bytes<KIND>() + DOWN_CHUNK_G * slot};
+
+  // the whole group table, the routing weights and the shared gate in one trip
   if (tid == 0) s_groups = *ws.n_groups;
-  __syncthreads();
-  const int groups = s_groups;
-  const int first = by * DOWN_GROUPS;
-  if (first >= groups) return;
-  if (tid < DOWN_GROUPS) {
-    const int gi = first + tid;
-    s_n[tid] = gi < groups ? ws.g_ntok[gi] : 0;
-    s_e[tid] = gi < groups ? ws.g_expert[gi] : 0;
-  }
-  __syncthreads();
-  if (tid < DOWN_GROUPS * NT) {
-    const int w = tid / NT, t = tid % NT;
-    if (t < s_n[w]) {
-      const int p = ws.g_pair[(first + w) * 16 + t];
-      s_pair[w][t] = p;
-      s_xrow[w][t] = (const XT*)ws.h + (int64_t)p * F;
-    }
-  }
-  __syncthreads();
-  const int n_tok = s_n[wave], e = s_e[wave];
-  const uint8_t* src = (e == E ? sh_down : down + (int64_t)e * D * rb) + (int64_t)row0 * rb;
-  ByteStage<4> wst(wt, src, n_tok ? (int)(16 * rb) : 0, nullptr, nullptr, 0);
-  XStage<KIND, XT, MT, 8> xst(xs, s_xrow[wave], n_tok, F);
-  wst.load(0, lane, 64);
-  xst.load(0, lane, 64);
-  wst.store(0, lane, 64);
-  xst.store(0, lane, 64);
-  for (int p = 1; p < wst.passes(64); ++p) {
-    wst.load(p, lane, 64);
-    wst.store(p, lane, 64);
-  }
-  for (int p = 1; p < xst.passes(64); ++p) {
-    xst.load(p, lane, 64);
-    xst.store(p, lane, 64);
-  }
+  if (tid < B) s_gsh[tid] = ws.gsh[tid];
+  copy_to_lds<1>(s_e, ws.g_expert, G, tid, 256);
+  copy_to_lds<1>(s_n, ws.g_ntok, G, tid, 256);
+  copy_to_lds<1>(s_w, ws.w, P, tid, 256);
+  copy_to_lds<11>(&s_pair[0][0], ws.g_pair, G * 16, tid, 256);
   if constexpr (KIND == IQ3_S) {
-    ByteStage<4> tst(tab, signed_tab, IQ3S_SIGNED_BYTES, nullptr, nullptr, 0);
+    ByteStage<8> tst(tab, signed_tab, IQ3S_SIGNED_BYTES, nullptr, nullptr, 0);
     for (int p = 0; p < tst.passes(256); ++p) {
       tst.load(p, tid, 256);
       tst.store(p, tid, 256);
     }
   }
   __syncthreads();
-  if (n_tok) {
-    float acc[TPG];
-#pragma unroll
-    for (int i = 0; i < TPG; ++i) acc[i] = 0.0f;
-    tile_mac<KIND, MT, TPG>(wt + lead_of(src), (int)rb, xs, F, n_tok, 0, F / scale_group<KIND>(), (const uint32_t*)tab, acc);
-    const int g = lane >> 4, n = lane & 15;
-#pragma unroll
-    for (int i = 0; i < TPG; ++i) {
-      const int t = g * TPG + i;
-      if (t < n_tok) ((XT*)ws.y)[(int64_t)s_pair[wave][t] * D + row0 + n] = from_f32<XT>(acc[i]);
+  const int groups = s_groups;
+  const int chunks = (groups + DOWN_CHUNK_G - 1) / DOWN_CHUNK_G;
+  auto sources = [&](int c) {
+    const int g0 = c * DOWN_CHUNK_G;
+    if (tid < DOWN_CHUNK_G && g0 + tid < groups) {
+      const int e = s_e[g0 + tid];
+      s_src[c & 1][tid] = (e == E ? sh_down : down + (int64_t)e * D * rb) + (int64_t)row0 * rb;
     }
-  }
-  // the last block of this row tile to finish combines it
-  __threadfence();
+  };
+  sources(0);
   __syncthreads();
-  if (tid == 0) {
-    const int batches = (groups + DOWN_GROUPS - 1) / DOWN_GROUPS;
-    s_last = atomicAdd(&ws.counter[blockIdx.x], 1) == batches - 1;
+  SliceStage<10> st(buf[0], s_src[0], min(DOWN_CHUNK_G, groups), (int)(16 * rb), slot);
+  for (int p = 0; p < st.passes(); ++p) {
+    st.load(p, tid);
+    st.store(p, tid);
   }
+  if (chunks > 1) sources(1);
   __syncthreads();
-  if (!s_last) return;
-  __threadfence();
-  if (tid == 0) ws.counter[blockIdx.x] = 0;
+  for (int c = 0; c < chunks; ++c) {
+    // the next chunk's loads go out before this chunk multiplies
+    const bool more = c + 1 < chunks;
+    SliceStage<10> nx(buf[(c + 1) & 1], s_src[(c + 1) & 1], more ? min(DOWN_CHUNK_G, groups - (c + 1) * DOWN_CHUNK_G) : 0,
+                      (int)(16 * rb), slot);
+    const int single = nx.passes() == 1;
+    if (more && single) nx.load(0, tid);
+    const int g0 = c * DOWN_CHUNK_G, gn = min(DOWN_CHUNK_G, groups - g0);
+    for (int li = wave; li < gn; li += 4) {
+      const int gi = g0 + li;
+      const int n_tok = s_n[gi];
+      const int mt = lane_token<TPG>();
+      const bool real = mt < n_tok;
+      const MT* xg = (const MT*)ws.h + (int64_t)s_pair[gi][real ? mt : 0] * F;
+      float acc[1][TPG];
+#pragma unroll
+      for (int i = 0; i < TPG; ++i) acc[0][i] = 0.0f;
+      const uint8_t* tiles[1] = {buf[c & 1] + li * slot + lead_of(s_src[c & 1][li])};
+      tile_mac_global<KIND, MT, TPG, frag_chunk<KIND>(), 1>(tiles, (int)rb, xg, real, 0, F / scale_group<KIND>(),
+                                                            (const uint32_t*)tab, acc);
+      const int g = lane >> 4, n = lane & 15;
+#pragma unroll
+      for (int i = 0; i < TPG; ++i) {
+        const int t = g * TPG + i;
+        if (t < n_tok) s_y[s_pair[gi][t]][n] = to_f32(from_f32<XT>(acc[0][i]));
+      }
+    }
+    if (more) {
+      if (single) {
+        nx.store(0, tid);
+      } else {
+        for (int p = 0; p < nx.passes(); ++p) {
+          nx.load(p, tid);
+          nx.store(p, tid);
+        }
+      }
+    }
+    __syncthreads();
+    if (c + 2 < chunks) sources(c + 2);
+    __syncthreads();
+  }
+  // the combine (strata_mlx/fused.py:448-462): experts in 8 rows j taking k = j, j + 8, ..., each product rounded
   if (tid < B * 16) {
-    const int t = tid >> 4, n = tid & 15, col = row0 + n;
-    const XT* y = (const XT*)ws.y;
+    const int t = tid >> 4, n = tid & 15;
     float acc = 0.0f;
     for (int j = 0; j < 8 && j < K; ++j) {
       float part = 0.0f;
       for (int kk = j; kk < K; kk += 8) {
-        const float prod = to_f32(y[(int64_t)(t * K + kk) * D + col]) * ws.w[t * K + kk];
+        const float prod = s_y[t * K + kk][n] * s_w[t * K + kk];
         part = prod + part;
       }
       acc = j == 0 ? part : part + acc;
     }
     const XT routed = from_f32<XT>(acc);
-    const XT gate = from_f32<XT>(1.0f / (1.0f + expf(-ws.gsh[t])));
-    const XT shared = from_f32<XT>(to_f32(gate) * to_f32(y[(int64_t)(B * K + t) * D + col]));
-    out[(int64_t)t * D + col] = from_f32<XT>(to_f32(routed) + to_f32(shared));
+    const XT gate = from_f32<XT>(1.0f / (1.0f + expf(-s_gsh[t])));
+    const XT shared = from_f32<XT>(to_f32(gate) * s_y[P + t][n]);
+    out[(int64_t)t * D + row0 + n] = from_f32<XT>(to_f32(routed) + to_f32(shared));
   }
 }
 
@@ -382,32 +463,36 @@ static int launch_moe(const uint8_t* gate, const uint8_t* up, const uint8_t* dow
                       const uint8_t* su, const uint8_t* sd, const XT* wg, const uint8_t* tables, const LT* logits,
                       const XT* x, int64_t B, int64_t K, int64_t D, int64_t F, XT* out, const MoeWs& ws,
                       hipStream_t stream, int phases) {
-  constexpr int NT = 4 * TPG;
   const uint8_t* stab = tables ? tables + TAB_IQ3S_SIGNED : nullptr;
   int st = OK;
   if (phases & 1) {
-    hipLaunchKernelGGL((k_moe_route<XT, LT>), dim3(1), dim3(256), 0, stream, logits, x, wg, (int)B, (int)E, (int)K, (int)D, ws);
-    st = check_launch("moe_decode route");
+    auto route = [&](auto vc) {
+      constexpr int V = decltype(vc)::value;
+      hipLaunchKernelGGL((k_moe_route<KIND, XT, LT, V>), dim3(1), dim3(256), 0, stream, logits, x, wg, (int)B, (int)E,
+                         (int)K, (int)D, ws);
+      return check_launch("moe_decode route");
+    };
+    const int vpl = (int)(E / 64);
+    st = vpl == 1 ? route(kind_c<1>{}) : vpl == 2 ? route(kind_c<2>{}) : vpl == 4 ? route(kind_c<4>{})
+       : vpl == 8 ? route(kind_c<8>{}) : vpl == 16 ? route(kind_c<16>{}) : route(kind_c<32>{});
     if (st) return st;
   }
-  if (!(phases & 2)) goto down_phase;
-  {
-  const size_t lds_gu = (size_t)moe_tab_bytes<KIND>() + (size_t)NT * D * sizeof(XT) + 2 * (16 * row_bytes(KIND, D) + 16);
-  hipLaunchKernelGGL((k_moe_gate_up<KIND, XT, TPG>), dim3((unsigned)(F / 16), (unsigned)(B * K + 1)), dim3(256), lds_gu,
-                     stream, gate, up, sg, su, (int)E, (int)K, (int)B, (int)D, (int)F, x, stab, ws);
-  st = check_launch("moe_decode gate_up");
-  if (st) return st;
+  if (phases & 2) {
+    const size_t lds = (size_t)moe_tab_bytes<KIND>() + 2 * (16 * row_bytes(KIND, D) + 16);
+    hipLaunchKernelGGL((k_moe_gate_up<KIND, KIND_DOWN, XT, TPG>), dim3((unsigned)(F / 16), (unsigned)(B * K + 1)),
+                       dim3(256), lds, stream, gate, up, sg, su, (int)E, (int)K, (int)B, (int)D, (int)F, stab, ws);
+    st = check_launch("moe_decode gate_up");
+    if (st) return st;
   }
-down_phase:
-  if (!(phases & 4)) return OK;
-  {
-  const size_t wave_bytes = (size_t)NT * F * sizeof(XT) + ((16 * row_bytes(KIND_DOWN, F) + 16 + 15) & ~(int64_t)15);
-  const size_t lds_d = (size_t)moe_tab_bytes<KIND_DOWN>() + 4 * wave_bytes;
-  const unsigned batches = (unsigned)((B * K + 1 + DOWN_GROUPS - 1) / DOWN_GROUPS);
-  hipLaunchKernelGGL((k_moe_down<KIND_DOWN, XT, TPG>), dim3((unsigned)(D / 16), batches), dim3(256), lds_d, stream, down,
-                     sd, (int)E, (int)K, (int)B, (int)D, (int)F, stab, ws, out);
-  return check_launch("moe_decode down");
+  if (phases & 4) {
+    const int64_t rbd = row_bytes(KIND_DOWN, F);
+    const size_t slot = (size_t)(((15 + 16 * rbd + 15) >> 4) << 4);
+    const size_t lds = (size_t)moe_tab_bytes<KIND_DOWN>() + 2 * DOWN_CHUNK_G * slot;
+    hipLaunchKernelGGL((k_moe_down<KIND_DOWN, XT, TPG>), dim3((unsigned)(D / 16)), dim3(256), lds, stream, down, sd,
+                       (int)E, (int)K, (int)B, (int)D, (int)F, stab, ws, out);
+    st = check_launch("moe_decode down");
   }
+  return st;
 }
 
 }  // namespace sh
@@ -425,10 +510,11 @@ int moe_decode(int phases, int kind, int kind_down, const void* gate, const void
   if (tokens > MOE_MAX_TOKENS || tokens * k > MOE_MAX_PAIRS || k <= 0 || k > 16)
     return fail(E_SHAPE, "moe_decode: %lld tokens of %lld experts (at most %d tokens, %d pairs)", (long long)tokens,
                 (long long)k, MOE_MAX_TOKENS, MOE_MAX_PAIRS);
-  if (experts <= 0 || experts % 64 || experts > 2048 || k > experts)
-    return fail(E_SHAPE, "moe_decode: %lld experts (a multiple of 64, at most 2048)", (long long)experts);
-  if (d_model % 256 || d_ff % 256 || d_model <= 0 || d_ff <= 0)
-    return fail(E_SHAPE, "moe_decode: widths %lld / %lld (multiples of 256)", (long long)d_model, (long long)d_ff);
+  if (experts <= 0 || vpl_bad(experts) || k > experts)
+    return fail(E_SHAPE, "moe_decode: %lld experts (64 times a power of two, at most 2048)", (long long)experts);
+  if (d_model % 256 || d_ff % 256 || d_model <= 0 || d_ff <= 0 || d_model > MOE_MAX_D)
+    return fail(E_SHAPE, "moe_decode: widths %lld / %lld (multiples of 256, d_model at most %d)", (long long)d_model,
+                (long long)d_ff, MOE_MAX_D);
   if (!mfma_kind_host(kind) || !mfma_kind_host(kind_down))
     return fail(E_UNSUPPORTED, "moe_decode: kinds %d / %d (the fused step takes Q2_0 and IQ3_S)", kind, kind_down);
   if (!gate || !up || !down || !shared_gate || !shared_up || !shared_down || !shared_gate_w || !logits || !x || !out)

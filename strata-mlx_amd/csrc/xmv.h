@@ -213,6 +213,24 @@ template <int KIND, typename XT, typename MT, int UNROLL> struct XStage {
   }
 };
 
+// n values from global memory to LDS, every load of a thread's share issued before its stores
+template <int U, typename T>
+__device__ __forceinline__ void copy_to_lds(T* dst, const T* src, int n, int tid, int nthreads) {
+  for (int base = 0; base < n; base += U * nthreads) {
+    T v[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int i = base + u * nthreads + tid;
+      if (i < n) v[u] = src[i];
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int i = base + u * nthreads + tid;
+      if (i < n) dst[i] = v[u];
+    }
+  }
+}
+
 // ---- the tile multiply-accumulate: this wave's share of a 16-row tile's columns, for the block's tokens
 //
 // wrow0: LDS address of row 0 of the tile (row n at wrow0 + n * rbytes); xs: staged activations (token t at
@@ -271,6 +289,105 @@ __device__ __forceinline__ void tile_mac(const uint8_t* wrow0, int rbytes, const
       for (int i = 0; i < TPG; ++i) acc[i] = fmaf(db, D[i], acc[i]);
     }
   }
+}
+
+// Where activation k of a row goes in KIND's staged layout, and the factor it is staged with (a power of two):
+// Q2_0 permuted and scaled per slot, IQ3_S as it is. A producer that writes its output this way (the route's x,
+// gate/up's inner activations) lets the next kernel load its MFMA A fragments straight from memory.
+template <int KIND, typename MT> __device__ __forceinline__ int stage_index(int k, float& scale) {
+  if constexpr (KIND == Q2_0) {
+    int j;
+    const int pos = q2_stage_pos(k & 63, j);
+    scale = 1.0f / q2_unit<MT>(j);
+    return (k & ~63) + pos;
+  } else {
+    scale = 1.0f;
+    return k;
+  }
+}
+
+// NW weight tiles (16 rows each, row n of tile w at wrow0[w] + n * rbytes, in LDS) against one token's staged row in
+// memory (xg, global: L2-resident), CH scale groups at a time: every fragment load of a chunk is issued before its
+// MFMAs, and each fragment serves all NW tiles. acc[w][TPG] accumulates tile w.
+template <int KIND, typename MT, int TPG, int CH, int NW>
+__device__ __forceinline__ void tile_mac_global(const uint8_t* const* wrow0, int rbytes, const MT* xg, bool real,
+                                                int g_begin, int g_end, const uint32_t* stab, float (*acc)[TPG]) {
+  constexpr int PER = KIND == Q2_0 ? 2 : 1;  // fragments a scale group
+  const int lane = threadIdx.x & 63, g = lane >> 4, n = lane & 15;
+  const f32x4 zero4 = {0.0f, 0.0f, 0.0f, 0.0f};
+  for (int c0 = g_begin; c0 < g_end; c0 += CH) {
+    const int cn = min(CH, g_end - c0);
+    u32x4 fr[CH * PER];
+#pragma unroll
+    for (int i = 0; i < CH * PER; ++i) {
+      fr[i] = u32x4{0u, 0u, 0u, 0u};
+      if (real && i < cn * PER) {
+        const int sg = c0 + i / PER;
+        const int at = KIND == Q2_0 ? sg * 64 + (i % PER) * 32 + g * 8 : sg * 32 + g * 8;
+        fr[i] = *(const u32x4*)(xg + at);
+      }
+    }
+#pragma unroll
+    for (int w = 0; w < NW; ++w) {
+      const uint8_t* wrow = wrow0[w] + (size_t)n * rbytes;
+      if constexpr (KIND == Q2_0) {
+        const u32x4 corr = q2_correction<MT>();
+#pragma unroll
+        for (int i = 0; i < CH; ++i) {
+          if (i < cn) {
+            const uint8_t* b = wrow + (c0 + i) * 18;
+            const uint32_t W = (uint32_t)*(const uint16_t*)(b + 2 + 2 * g) | ((uint32_t)*(const uint16_t*)(b + 10 + 2 * g) << 16);
+            const float d = half_bits(*(const uint16_t*)b);
+            u32x4 fa, fb;
+            q2_decode<MT>(W, fa, fb);
+            f32x4 D = mfma<MT>(fr[2 * i], corr, zero4);
+            D = mfma<MT>(fr[2 * i + 1], corr, D);
+            D = mfma<MT>(fr[2 * i], fa, D);
+            D = mfma<MT>(fr[2 * i + 1], fb, D);
+#pragma unroll
+            for (int t = 0; t < TPG; ++t) acc[w][t] = fmaf(d, D[t], acc[w][t]);
+          }
+        }
+      } else {
+        const float cval = -(Magic<MT>::BASE + 16.0f);
+        const uint32_t c2 = pack2<MT>(cval, cval);
+        const u32x4 corr = {c2, c2, c2, c2};
+        constexpr uint32_t hi4 = Magic<MT>::HI * 0x01010101u;
+#pragma unroll
+        for (int i = 0; i < CH; ++i) {
+          if (i < cn) {
+            const int run = c0 + i;
+            const uint8_t* b = wrow + (run >> 3) * 110;
+            const int ib = run & 7;
+            const float db = half_bits(*(const uint16_t*)b) * (float)(1 + 2 * (((uint32_t)b[106 + ib / 2] >> (4 * (ib & 1))) & 15u));
+            const uint32_t q2 = *(const uint16_t*)(b + 2 + 8 * ib + 2 * g);
+            const uint32_t qh = (uint32_t)b[66 + ib] >> (2 * g);
+            const uint32_t sg = b[74 + 4 * ib + g];
+            const uint32_t e0 = stab[(q2 & 0xffu) | ((qh & 1u) << 8) | ((sg & 15u) << 9)];
+            const uint32_t e1 = stab[(q2 >> 8) | ((qh & 2u) << 7) | ((sg >> 4) << 9)];
+            u32x4 fw;
+            fw.x = __builtin_amdgcn_perm(hi4, e0, 0x04010400u);
+            fw.y = __builtin_amdgcn_perm(hi4, e0, 0x04030402u);
+            fw.z = __builtin_amdgcn_perm(hi4, e1, 0x04010400u);
+            fw.w = __builtin_amdgcn_perm(hi4, e1, 0x04030402u);
+            f32x4 D = mfma<MT>(fr[i], corr, zero4);
+            D = mfma<MT>(fr[i], fw, D);
+#pragma unroll
+            for (int t = 0; t < TPG; ++t) acc[w][t] = fmaf(db, D[t], acc[w][t]);
+          }
+        }
+      }
+    }
+  }
+}
+
+// scale groups a chunk of tile_mac_global takes (16 fragments)
+template <int KIND> __host__ __device__ constexpr int frag_chunk() { return KIND == Q2_0 ? 8 : 16; }
+
+// the token of the A row a lane supplies (4 * TPG if a padding row)
+template <int TPG> __device__ __forceinline__ int lane_token() {
+  const int n = threadIdx.x & 15;
+  return (n & 3) < TPG ? (n >> 2) * TPG + (n & 3) : 4 * TPG;
 }
 
 // scale groups of a row (Q2_0 blocks of 64 weights, IQ3_S runs of 32)

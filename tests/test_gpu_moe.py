@@ -15,12 +15,14 @@ from strata_hip import synth
 pytestmark = pytest.mark.gpu
 
 
-def layer(kind, kind_down, E, D, F, seed, dev, tables):
+def layer(kind, kind_down, E, D, F, seed, dev, tables, sigma=0.02):
     rng = np.random.default_rng(seed)
-    raw = {"gate": synth.random_blocks(kind, E * F, D, rng), "up": synth.random_blocks(kind, E * F, D, rng),
-           "down": synth.random_blocks(kind_down, E * D, F, rng),
-           "sgate": synth.random_blocks(kind, F, D, rng), "sup": synth.random_blocks(kind, F, D, rng),
-           "sdown": synth.random_blocks(kind_down, D, F, rng)}
+
+    def blocks(k, rows, cols):
+        return synth.random_blocks(k, rows, cols, rng, sigma=sigma)
+
+    raw = {"gate": blocks(kind, E * F, D), "up": blocks(kind, E * F, D), "down": blocks(kind_down, E * D, F),
+           "sgate": blocks(kind, F, D), "sup": blocks(kind, F, D), "sdown": blocks(kind_down, D, F)}
     kinds = {"gate": kind, "up": kind, "down": kind_down, "sgate": kind, "sup": kind, "sdown": kind_down}
     shapes = {"gate": (E, F, D), "up": (E, F, D), "down": (E, D, F), "sgate": (1, F, D), "sup": (1, F, D),
               "sdown": (1, D, F)}
@@ -34,7 +36,10 @@ def layer(kind, kind_down, E, D, F, seed, dev, tables):
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 def test_moe_decode_is_the_oracles_block(kinds, tokens, dtype, tables, dev):
     E, D, F, K = 64, 512, 256, 10
-    lin, w, rng = layer(*kinds, E, D, F, tokens, dev, tables)
+    # IQ3_S weights reach 465 times their block scale: with fp16 activations smaller scales keep the block's values
+    # finite (the oracle, like the reference, overflows otherwise)
+    sigma = 0.002 if dtype == torch.float16 else 0.02
+    lin, w, rng = layer(*kinds, E, D, F, tokens, dev, tables, sigma)
     name = "bfloat16" if dtype == torch.bfloat16 else "float16"
     x = torch.from_numpy(rng.standard_normal((tokens, D)).astype(np.float32)).to(dtype)
     logits = torch.from_numpy(rng.standard_normal((tokens, E)).astype(np.float32)).to(dtype)
@@ -49,6 +54,7 @@ def test_moe_decode_is_the_oracles_block(kinds, tokens, dtype, tables, dev):
                                            wg.float().numpy(), name)
     np.testing.assert_array_equal(idx.cpu().numpy(), want_idx)
     np.testing.assert_allclose(wt.cpu().numpy(), want_w, rtol=2e-6, atol=1e-7)
+    assert np.isfinite(want).all()
     assert rel_err(out.float().cpu(), want) <= 1e-2
 
 
