@@ -69,6 +69,54 @@ def build_layers(n_layers, dev, kind):
     return layers, raw
 
 
+def matvec_stream(dev, steps, warmup):
+    """C2: 3072 x 2048 matvecs straight from GGUF blocks, as streaming throughput over distinct matrices (a stack of
+    more than 600 MB, past the 256 MB Infinity Cache, in one launch) and as one matrix alone, B = 1, 4, 8 bf16."""
+    import torch
+
+    from strata_hip import blocks as SB
+    from strata_hip import synth
+
+    R, C = 3072, 2048
+    res = {}
+    for kind in ("Q2_0", "IQ3_S"):
+        mat = R * SB.row_bytes(kind, C)
+        n = -(-600_000_000 // mat)
+        blocks = synth.random_blocks_gpu(kind, n * R, C, 7, dev)
+        res[kind] = {}
+        for b in (1, 4, 8):
+            x = torch.randn(n, b, C, device=dev).to(torch.bfloat16)
+            one = x[:1].contiguous()
+            out = {}
+            for name, nm, xx in (("stream", n, x), ("single", 1, one)):
+                SB.stack_matvec(blocks, kind, (nm, R, C), xx)
+                g = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(g):
+                    for _ in range(1 if name == "stream" else 20):
+                        SB.stack_matvec(blocks, kind, (nm, R, C), xx)
+                for _ in range(warmup):
+                    g.replay()
+                torch.cuda.synchronize()
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                e0.record()
+                for _ in range(steps):
+                    g.replay()
+                e1.record()
+                torch.cuda.synchronize()
+                calls = steps * (1 if name == "stream" else 20)
+                sec = e0.elapsed_time(e1) * 1e-3 / calls
+                nbytes = nm * (mat + b * C * 2 + b * R * 2)
+                out[name] = (sec, nbytes)
+            ss, sb = out["stream"]
+            us, ub = out["single"]
+            res[kind][str(b)] = {"stream_GBps": round(sb / ss / 1e9, 1), "stream_frac": round(sb / ss / 1e9 / HBM_PEAK_GBS, 4),
+                                 "matrices": n, "single_us": round(us * 1e6, 2), "single_GBps": round(ub / us / 1e9, 1)}
+            print(f"# C2 {kind} B={b}: {res[kind][str(b)]}", file=sys.stderr, flush=True)
+        del blocks
+        torch.cuda.empty_cache()
+    return res
+
+
 def cpu_baseline(raw, inputs, kind, seconds, check_outputs):
     """The oracle's restatement of the reference's CPU path (dequantize the touched experts, numpy matmul in
     float32, the reference's routing, SwiGLU and combine roundings), one thread, on the host cores."""
@@ -135,6 +183,7 @@ def main():
     ap.add_argument("--kind", default="Q2_0")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--no-matvec", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: --gpus {args.gpus}: this path is measured on one GPU (expert parallelism across GPUs is "
@@ -218,6 +267,7 @@ def main():
         inputs[b] = list(zip(logits, xs, outs))
         print(f"# B={b}: {per_batch[b]}", file=sys.stderr, flush=True)
 
+    matvec = None if args.no_matvec else matvec_stream(dev, max(3, args.steps // 4), args.warmup)
     value = all_bytes / all_time / 1e9
     achieved = gu_bytes / gu_time / 1e9
     traffic = None
@@ -236,6 +286,7 @@ def main():
                    "d_ff": F, "top_k": K, "batches": batches, "layers_per_pass": args.layers,
                    "step": "one decode pass through the layers at each batch width"},
         "per_batch": {str(k): v for k, v in per_batch.items()},
+        "matvec_3072x2048": matvec,
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic, "kernel": "k_moe_gate_up",
                      "bytes_per_launch": round(gu_bytes / gu_launches), "launches": gu_launches,

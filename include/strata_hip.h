@@ -75,6 +75,14 @@ int sh_switch_matvec_generic(int kind, const void* blocks, const void* const* ex
                              int64_t experts, int64_t rows, int64_t cols, const int32_t* idx, int64_t pairs,
                              const void* x, int x_dtype, int64_t share, void* out, void* stream);
 
+/* strata_mlx/blocks.py:351-394 (window_matvec) over a stack: out[m][t] = W_m . x[m][t], x (n_mats, tokens <= 16,
+ * cols) bf16 / fp16, out (n_mats, tokens, rows); Q2_0 or IQ3_S, cols a multiple of 256. One streaming launch over
+ * all matrices (and a staging launch for x). workspace: sh_stack_workspace() bytes. */
+size_t sh_stack_workspace(int kind, int64_t n_mats, int64_t rows, int64_t cols, int64_t tokens, int x_dtype);
+int sh_stack_matvec(int kind, const void* blocks, const void* tables, int64_t n_mats, int64_t rows, int64_t cols,
+                    const void* x, int x_dtype, int64_t tokens, void* out, void* workspace, size_t workspace_bytes,
+                    void* stream);
+
 /* strata_mlx/blocks.py:331-346 (matvec_separate): one expert buffer per pair, `expert_ptrs` a device array of
  * `pairs` pointers. */
 int sh_matvec_separate(int kind, const void* const* expert_ptrs, const void* tables, int64_t rows, int64_t cols,

@@ -231,6 +231,127 @@ __device__ __forceinline__ void copy_to_lds(T* dst, const T* src, int n, int tid
   }
 }
 
+// the token of the A row a lane supplies (4 * TPG if a padding row)
+template <int TPG> __device__ __forceinline__ int lane_token() {
+  const int n = threadIdx.x & 15;
+  return (n & 3) < TPG ? (n >> 2) * TPG + (n & 3) : 4 * TPG;
+}
+
+// XStage that also leaves, per scale group of each row, the sum the magic-number decode's constant offsets add
+// (Q2_0: sum_k (BASE + U_k) xs_k; IQ3_S: sum_k (BASE + 16) x_k) at corr[t * ngroups + group]: the eight (Q2_0) or
+// four (IQ3_S) threads of a group hold consecutive vectors and meet by __shfl_xor. nthreads % 64 == 0.
+template <int KIND, typename XT, typename MT, int UNROLL> struct XStageCorr {
+  static_assert(sizeof(XT) == 2, "16-bit activations");
+  const XT* base;
+  MT* xs;
+  float* corr;
+  int cols, per_row, total;
+  u32x4 v[UNROLL];
+
+  // row t of the activations at base + t * cols
+  __device__ __forceinline__ XStageCorr(MT* xs_, float* corr_, const XT* base_, int n_tok, int cols_)
+      : base(base_), xs(xs_), corr(corr_), cols(cols_), per_row(cols_ >> 3), total(n_tok * (cols_ >> 3)) {}
+  __device__ __forceinline__ int passes(int nthreads) const { return (total + UNROLL * nthreads - 1) / (UNROLL * nthreads); }
+  __device__ __forceinline__ void load(int pass, int tid, int nthreads) {
+#pragma unroll
+    for (int u = 0; u < UNROLL; ++u) {
+      const int i = (pass * UNROLL + u) * nthreads + tid;
+      if (i < total) {
+        v[u] = *(const u32x4*)(base + 8 * (int64_t)i);  // rows are contiguous: vector i of the block
+      }
+    }
+  }
+  __device__ __forceinline__ void store(int pass, int tid, int nthreads) {
+    constexpr int SG = KIND == Q2_0 ? 64 : 32, LANES = SG / 8;
+#pragma unroll
+    for (int u = 0; u < UNROLL; ++u) {
+      const int i = (pass * UNROLL + u) * nthreads + tid;  // i and its group's other vectors: consecutive threads
+      float part = 0.0f;
+      if (i < total) {
+        const int t = i / per_row, c8 = i - t * per_row;
+        MT* dst = xs + (size_t)t * cols;
+        const XT* vals = (const XT*)&v[u];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const int k = 8 * c8 + e;
+          if constexpr (KIND == Q2_0) {
+            int j;
+            const int pos = q2_stage_pos(k & 63, j);
+            const MT staged = from_f32<MT>(to_f32(vals[e]) * (1.0f / q2_unit<MT>(j)));
+            dst[(k & ~63) + pos] = staged;
+            part += (Magic<MT>::BASE + q2_unit<MT>(j)) * to_f32(staged);
+          } else {
+            dst[k] = vals[e];
+            part += (Magic<MT>::BASE + 16.0f) * to_f32(vals[e]);
+          }
+        }
+      }
+#pragma unroll
+      for (int o = LANES >> 1; o > 0; o >>= 1) part += __shfl_xor(part, o);
+      if (i < total && (tid & (LANES - 1)) == 0) {
+        const int t = i / per_row, c8 = i - t * per_row;
+        corr[t * (cols / SG) + (8 * c8) / SG] = part;
+      }
+    }
+  }
+};
+
+// One wave's 16-row tile x [g_begin, g_end) scale groups against activations staged in LDS by XStageCorr: the
+// accumulator starts at minus the offsets' sum of its token, so a Q2_0 block takes 2 MFMAs and an IQ3_S run 1.
+// Fragments and sums are read from LDS a scale group at a time.
+template <int KIND, typename MT, int TPG>
+__device__ __forceinline__ void tile_mac_lds(const uint8_t* wrow0, int rbytes, const MT* xs, const float* corr,
+                                             int cols, int ngroups, int n_tok, int g_begin, int g_end,
+                                             const uint32_t* stab, float* acc) {
+  const int lane = threadIdx.x & 63, g = lane >> 4, n = lane & 15;
+  const int mt = lane_token<TPG>();
+  const bool areal = mt < n_tok;
+  const uint8_t* wrow = wrow0 + (size_t)n * rbytes;
+  const MT* xt = xs + (size_t)(areal ? mt : 0) * cols;
+  const u32x4 zfrag = {0u, 0u, 0u, 0u};
+  bool dreal[TPG];
+#pragma unroll
+  for (int t = 0; t < TPG; ++t) dreal[t] = g * TPG + t < n_tok;
+  for (int sg = g_begin; sg < g_end; ++sg) {
+    f32x4 C = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int t = 0; t < TPG; ++t)
+      if (dreal[t]) C[t] = -corr[(g * TPG + t) * ngroups + sg];
+    if constexpr (KIND == Q2_0) {
+      const uint8_t* b = wrow + sg * 18;
+      const uint32_t W = (uint32_t)*(const uint16_t*)(b + 2 + 2 * g) | ((uint32_t)*(const uint16_t*)(b + 10 + 2 * g) << 16);
+      const float d = half_bits(*(const uint16_t*)b);
+      u32x4 fa, fb;
+      q2_decode<MT>(W, fa, fb);
+      const u32x4 xa = areal ? *(const u32x4*)(xt + sg * 64 + g * 8) : zfrag;
+      const u32x4 xb = areal ? *(const u32x4*)(xt + sg * 64 + 32 + g * 8) : zfrag;
+      f32x4 D = mfma<MT>(xa, fa, C);
+      D = mfma<MT>(xb, fb, D);
+#pragma unroll
+      for (int t = 0; t < TPG; ++t) acc[t] = fmaf(d, D[t], acc[t]);
+    } else {
+      constexpr uint32_t hi4 = Magic<MT>::HI * 0x01010101u;
+      const uint8_t* b = wrow + (sg >> 3) * 110;
+      const int ib = sg & 7;
+      const float db = half_bits(*(const uint16_t*)b) * (float)(1 + 2 * (((uint32_t)b[106 + ib / 2] >> (4 * (ib & 1))) & 15u));
+      const uint32_t q2 = *(const uint16_t*)(b + 2 + 8 * ib + 2 * g);
+      const uint32_t qh = (uint32_t)b[66 + ib] >> (2 * g);
+      const uint32_t sgn = b[74 + 4 * ib + g];
+      const uint32_t e0 = stab[(q2 & 0xffu) | ((qh & 1u) << 8) | ((sgn & 15u) << 9)];
+      const uint32_t e1 = stab[(q2 >> 8) | ((qh & 2u) << 7) | ((sgn >> 4) << 9)];
+      u32x4 fw;
+      fw.x = __builtin_amdgcn_perm(hi4, e0, 0x04010400u);
+      fw.y = __builtin_amdgcn_perm(hi4, e0, 0x04030402u);
+      fw.z = __builtin_amdgcn_perm(hi4, e1, 0x04010400u);
+      fw.w = __builtin_amdgcn_perm(hi4, e1, 0x04030402u);
+      const u32x4 xa = areal ? *(const u32x4*)(xt + sg * 32 + g * 8) : zfrag;
+      const f32x4 D = mfma<MT>(xa, fw, C);
+#pragma unroll
+      for (int t = 0; t < TPG; ++t) acc[t] = fmaf(db, D[t], acc[t]);
+    }
+  }
+}
+
 // ---- the tile multiply-accumulate: this wave's share of a 16-row tile's columns, for the block's tokens
 //
 // wrow0: LDS address of row 0 of the tile (row n at wrow0 + n * rbytes); xs: staged activations (token t at
@@ -381,14 +502,86 @@ __device__ __forceinline__ void tile_mac_global(const uint8_t* const* wrow0, int
   }
 }
 
+// NW weight tiles against one token row of staged activations (xg, in memory) whose offsets' sums were computed
+// with the staging (corr: token t's sums at corr_rows + t * ngroups): the accumulator starts at minus the sum, so a
+// Q2_0 block takes 2 MFMAs and an IQ3_S run 1. D rows hold tokens g * TPG + t (t < TPG), real below n_tok.
+template <int KIND, typename MT, int TPG, int CH, int NW>
+__device__ __forceinline__ void tile_mac_staged(const uint8_t* const* wrow0, int rbytes, const MT* xg, bool areal,
+                                                const float* corr_rows, int ngroups, int n_tok, int g_begin, int g_end,
+                                                const uint32_t* stab, float (*acc)[TPG]) {
+  constexpr int PER = KIND == Q2_0 ? 2 : 1;  // fragments a scale group
+  const int lane = threadIdx.x & 63, g = lane >> 4, n = lane & 15;
+  for (int c0 = g_begin; c0 < g_end; c0 += CH) {
+    const int cn = min(CH, g_end - c0);
+    u32x4 fr[CH * PER];
+    f32x4 cinit[CH];
+#pragma unroll
+    for (int i = 0; i < CH * PER; ++i) {
+      fr[i] = u32x4{0u, 0u, 0u, 0u};
+      if (areal && i < cn * PER) {
+        const int sg = c0 + i / PER;
+        const int at = KIND == Q2_0 ? sg * 64 + (i % PER) * 32 + g * 8 : sg * 32 + g * 8;
+        fr[i] = *(const u32x4*)(xg + at);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < CH; ++i) {
+      cinit[i] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int t = 0; t < TPG; ++t) {
+        const int tok = g * TPG + t;
+        if (i < cn && tok < n_tok) cinit[i][t] = -corr_rows[(int64_t)tok * ngroups + c0 + i];
+      }
+    }
+#pragma unroll
+    for (int w = 0; w < NW; ++w) {
+      const uint8_t* wrow = wrow0[w] + (size_t)n * rbytes;
+      if constexpr (KIND == Q2_0) {
+#pragma unroll
+        for (int i = 0; i < CH; ++i) {
+          if (i < cn) {
+            const uint8_t* b = wrow + (c0 + i) * 18;
+            const uint32_t W = (uint32_t)*(const uint16_t*)(b + 2 + 2 * g) | ((uint32_t)*(const uint16_t*)(b + 10 + 2 * g) << 16);
+            const float d = half_bits(*(const uint16_t*)b);
+            u32x4 fa, fb;
+            q2_decode<MT>(W, fa, fb);
+            f32x4 D = mfma<MT>(fr[2 * i], fa, cinit[i]);
+            D = mfma<MT>(fr[2 * i + 1], fb, D);
+#pragma unroll
+            for (int t = 0; t < TPG; ++t) acc[w][t] = fmaf(d, D[t], acc[w][t]);
+          }
+        }
+      } else {
+        constexpr uint32_t hi4 = Magic<MT>::HI * 0x01010101u;
+#pragma unroll
+        for (int i = 0; i < CH; ++i) {
+          if (i < cn) {
+            const int run = c0 + i;
+            const uint8_t* b = wrow + (run >> 3) * 110;
+            const int ib = run & 7;
+            const float db = half_bits(*(const uint16_t*)b) * (float)(1 + 2 * (((uint32_t)b[106 + ib / 2] >> (4 * (ib & 1))) & 15u));
+            const uint32_t q2 = *(const uint16_t*)(b + 2 + 8 * ib + 2 * g);
+            const uint32_t qh = (uint32_t)b[66 + ib] >> (2 * g);
+            const uint32_t sg = b[74 + 4 * ib + g];
+            const uint32_t e0 = stab[(q2 & 0xffu) | ((qh & 1u) << 8) | ((sg & 15u) << 9)];
+            const uint32_t e1 = stab[(q2 >> 8) | ((qh & 2u) << 7) | ((sg >> 4) << 9)];
+            u32x4 fw;
+            fw.x = __builtin_amdgcn_perm(hi4, e0, 0x04010400u);
+            fw.y = __builtin_amdgcn_perm(hi4, e0, 0x04030402u);
+            fw.z = __builtin_amdgcn_perm(hi4, e1, 0x04010400u);
+            fw.w = __builtin_amdgcn_perm(hi4, e1, 0x04030402u);
+            const f32x4 D = mfma<MT>(fr[i], fw, cinit[i]);
+#pragma unroll
+            for (int t = 0; t < TPG; ++t) acc[w][t] = fmaf(db, D[t], acc[w][t]);
+          }
+        }
+      }
+    }
+  }
+}
+
 // scale groups a chunk of tile_mac_global takes (16 fragments)
 template <int KIND> __host__ __device__ constexpr int frag_chunk() { return KIND == Q2_0 ? 8 : 16; }
-
-// the token of the A row a lane supplies (4 * TPG if a padding row)
-template <int TPG> __device__ __forceinline__ int lane_token() {
-  const int n = threadIdx.x & 15;
-  return (n & 3) < TPG ? (n >> 2) * TPG + (n & 3) : 4 * TPG;
-}
 
 // scale groups of a row (Q2_0 blocks of 64 weights, IQ3_S runs of 32)
 template <int KIND> __host__ __device__ constexpr int scale_group() { return KIND == Q2_0 ? 64 : 32; }

@@ -41,12 +41,14 @@ PROTOTYPES = {
     "sh_moe_workspace": [c_i64, c_i64, c_i64, c_i64, c_int],
     "sh_moe_decode": [c_int, c_int, c_vp, c_vp, c_vp, c_i64, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_int, c_vp, c_int,
                       c_i64, c_i64, c_i64, c_i64, c_vp, c_vp, c_vp, c_vp, c_sz, c_vp],
+    "sh_stack_workspace": [c_int, c_i64, c_i64, c_i64, c_i64, c_int],
+    "sh_stack_matvec": [c_int, c_vp, c_vp, c_i64, c_i64, c_i64, c_vp, c_int, c_i64, c_vp, c_vp, c_sz, c_vp],
     "sh_moe_decode_phase": [c_int, c_int, c_int, c_vp, c_vp, c_vp, c_i64, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_int,
                             c_vp, c_int, c_i64, c_i64, c_i64, c_i64, c_vp, c_vp, c_sz, c_vp],
 }
 _RESTYPE = {"sh_last_error": ctypes.c_char_p, "sh_tables_bytes": c_sz, "sh_tiles_workspace": c_sz,
             "sh_tiles_most": c_i64, "sh_switch_workspace": c_sz,
-            "sh_moe_workspace": c_sz}
+            "sh_moe_workspace": c_sz, "sh_stack_workspace": c_sz}
 
 _lib = None
 

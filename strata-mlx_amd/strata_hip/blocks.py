@@ -137,12 +137,41 @@ def matvec_separate(experts: list, kind: str, rows: int, cols: int, x: torch.Ten
     return out
 
 
+def stack_takes(kind: str, cols: int, dtype: torch.dtype) -> bool:
+    """Whether stack_matvec (the MFMA path) takes matrices of `kind` with rows of `cols` and `dtype` activations."""
+    return kind in ("Q2_0", "IQ3_S") and cols % 256 == 0 and dtype in (torch.bfloat16, torch.float16)
+
+
+def stack_matvec(blocks: torch.Tensor, kind: str, shape: tuple, x: torch.Tensor) -> torch.Tensor:
+    """out[m, t] = W_m . x[m, t] for a stack of `shape` (matrices, rows, cols) and x (matrices, tokens <= 16, cols)
+    bf16 / fp16: the window matvec (strata_mlx/blocks.py:351-394) over many matrices in one launch, streaming their
+    blocks. Returns (matrices, tokens, rows) in x's type."""
+    n, rows, cols = shape
+    if not stack_takes(kind, cols, x.dtype):
+        raise ValueError(f"stack_matvec: {kind}, {cols} columns, {x.dtype} (Q2_0 / IQ3_S, cols % 256, bf16 / fp16)")
+    x = x.reshape(n, -1, cols).contiguous()
+    tokens = x.shape[1]
+    if blocks.numel() < n * rows * row_bytes(kind, cols):
+        raise ValueError(f"blocks: {blocks.numel()} bytes for a {kind} stack of {tuple(shape)}")
+    _on_gpu(blocks, x)
+    out = torch.empty((n, tokens, rows), dtype=x.dtype, device=x.device)
+    k, dt = _kind(kind), _lib.dtype_code(x.dtype)
+    ws_bytes = _lib.load().sh_stack_workspace(k, n, rows, cols, tokens, dt)
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=x.device)
+    _lib.call("sh_stack_matvec", k, _u8(blocks).data_ptr(), _tabs(kind, x.device), n, rows, cols, x.data_ptr(), dt,
+              tokens, out.data_ptr(), ws.data_ptr(), ws_bytes, _lib.stream_of(x))
+    return out
+
+
 def window_matvec(blocks: torch.Tensor, kind: str, rows: int, cols: int, x: torch.Tensor,
                   per_row: int | None = None) -> torch.Tensor:
     """out[t] = W . x[t] for one layer `blocks` of (rows, cols) and x (tokens, cols). Returns (tokens, rows)
-    (strata_mlx/blocks.py:384-394). `per_row` is accepted for the interface; the library chooses its lanes."""
+    (strata_mlx/blocks.py:384-394). `per_row` is accepted for the interface; the library chooses its lanes. A token's
+    bits do not depend on the window it is in, on either path."""
     x = x.reshape(-1, cols).contiguous()
     tokens = x.shape[0]
+    if stack_takes(kind, cols, x.dtype) and 0 < tokens <= 16:
+        return stack_matvec(blocks, kind, (1, rows, cols), x[None])[0]
     _on_gpu(blocks, x)
     out = torch.empty((tokens, rows), dtype=x.dtype, device=x.device)
     for a in range(0, tokens, 8):

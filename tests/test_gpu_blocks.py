@@ -170,3 +170,29 @@ def test_lookup_matvec_is_the_product(tables, dev):
     table = SB.lookup_table(x.to(dev))
     got = SB.lookup_matvec(lin, torch.from_numpy(idx).to(dev), table, 2).float().cpu()
     assert rel_err(got, OB.matvec(w, idx, xv, 2)) <= 1e-2
+
+
+@pytest.mark.parametrize("kind", ["Q2_0", "IQ3_S"])
+@pytest.mark.parametrize("dtype", ["bfloat16", "float16"])
+@pytest.mark.parametrize("tokens", [1, 4, 8, 16])
+def test_stack_matvec_streams_many_matrices(kind, dtype, tokens, tables, dev):
+    """The streaming window matvec: every matrix of a stack times its own tokens, rows not a multiple of a tile."""
+    n, R, C = 7, 200, 512
+    raw, w = stack(kind, n, R, C, 20 + tokens, tables)
+    rng = np.random.default_rng(tokens)
+    x, xv = act(rng, (n, tokens, C), dtype)
+    got = SB.stack_matvec(torch.from_numpy(raw).to(dev), kind, (n, R, C), x.to(dev)).float().cpu().numpy()
+    want = np.einsum("mrc,mtc->mtr", w.astype(np.float64), xv.astype(np.float64))
+    assert got.shape == (n, tokens, R)
+    assert rel_err(got, want) <= TOL[dtype]
+
+
+@pytest.mark.parametrize("kind", ["Q2_0", "IQ3_S"])
+def test_window_matvec_bits_do_not_depend_on_the_window(kind, tables, dev):
+    raw, w = stack(kind, 1, 96, 2048, 30, tables)
+    x = torch.randn(8, 2048).to(torch.bfloat16)
+    b = torch.from_numpy(raw).to(dev)
+    got = SB.window_matvec(b, kind, 96, 2048, x.to(dev)).cpu()
+    alone = torch.cat([SB.window_matvec(b, kind, 96, 2048, x[t:t + 1].to(dev)).cpu() for t in range(8)])
+    assert torch.equal(alone, got)
+    assert rel_err(got.float(), x.float().numpy().astype(np.float64) @ w[0].T.astype(np.float64)) <= 1e-2
