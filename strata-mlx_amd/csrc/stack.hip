@@ -3,12 +3,16 @@
 // window of T <= 8 tokens, each run unpacked once for all of them) taken over many matrices in one launch, the form
 // in which a decode pass streams its weights.
 //
-// A persistent grid; an item is IR = 16 * WAVES / KW rows of one matrix (WAVES / KW waves take 16 rows each, KW
-// waves split the columns) and a block takes a contiguous run of items. A block stages its matrix's activations in
-// LDS in the order the MFMA fragments take them, with the sums the magic-number decode's offsets add (XStageCorr),
-// again only when the matrix changes. The next item's weight bytes (and activations, at a change of matrix) are
-// loaded into registers while this item multiplies from LDS, then stored over it: one LDS buffer, the registers the
-// second. Two shapes: streaming (64-row items) for many matrices, and 16-row items split four ways for few.
+// A block is RG x KW waves: RG row groups of 16 rows, the columns split KW ways, each wave owning GPER scale groups
+// of every row it multiplies. An item is IR = 16 * RG rows of one matrix; a block takes a contiguous run of items
+// and keeps NBUF of them in an LDS ring, filled by direct 16-byte loads into LDS (no registers, no stores), so
+// NBUF - 1 items are in flight while one is multiplied. Rows sit in LDS at a stride padded (when a row is whole
+// 16-byte chunks) so the 16 rows a wave reads fall in distinct banks.
+//
+// A wave's activation fragments for its columns, and minus the sums the magic-number decode's offsets add, live in
+// registers, loaded from global memory once per matrix: the multiply reads only weight bytes from LDS (three 16-bit
+// reads a Q2_0 block), fully unrolled over the wave's GPER groups. An IQ3_S block also holds the 32 KiB table of
+// signed grid entries in LDS.
 #include <type_traits>
 
 #include "launch.h"
@@ -16,121 +20,315 @@
 
 namespace sh {
 
-template <int KIND, typename XT, int TPG, int WAVES, int KW, int UW, int UX>
-__global__ __launch_bounds__(WAVES * 64) void k_stack_mv(const uint8_t* __restrict__ blocks, int64_t mat_bytes,
-                                                         int rows, int cols, int64_t rbytes, const XT* __restrict__ x,
-                                                         int tokens, XT* __restrict__ out,
-                                                         const uint8_t* __restrict__ signed_tab, int n_items) {
-  using MT = XT;
-  constexpr int NT = WAVES * 64, RG = WAVES / KW, IR = 16 * RG;
-  constexpr int TAB = KIND == IQ3_S ? IQ3S_SIGNED_BYTES : 0;
-  __shared__ float s_red[KW][RG][64][TPG];
-  extern __shared__ u32x4 dyn[];
-  const int ngroups = cols / scale_group<KIND>();
-  uint8_t* tab = (uint8_t*)dyn;
-  MT* xs = (MT*)(tab + TAB);
-  float* corr = (float*)(xs + (size_t)tokens * cols);
-  uint8_t* wt = (uint8_t*)(corr + ((tokens * ngroups + 3) & ~3));
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int rg = wave % RG, kh = wave / RG;
-  const int items_per_mat = (rows + IR - 1) / IR;
-  const int gper = ngroups / KW;
+constexpr int STACK_LMAX = 16;  // direct loads a thread an item, at most
 
-  const int per = (n_items + gridDim.x - 1) / gridDim.x;
-  const int first = blockIdx.x * per, last = min(n_items, first + per);
-  if (first >= last) return;
-  auto src_of = [&](int item, int& nbytes) {
-    const int m = item / items_per_mat, r0 = (item - m * items_per_mat) * IR;
-    nbytes = (int)(min(IR, rows - r0) * rbytes);
-    return blocks + (int64_t)m * mat_bytes + (int64_t)r0 * rbytes;
-  };
-  int nb;
-  const uint8_t* src = src_of(first, nb);
-  int m = first / items_per_mat;
-  {
-    ByteStage<UW> st(wt, src, nb, tab, signed_tab, TAB);
-    XStageCorr<KIND, XT, MT, UX> xst(xs, corr, x + (int64_t)m * tokens * cols, tokens, cols);
-    st.load(0, tid, NT);
-    xst.load(0, tid, NT);
-    st.store(0, tid, NT);
-    xst.store(0, tid, NT);
-    for (int p = 1; p < st.passes(NT); ++p) {
-      st.load(p, tid, NT);
-      st.store(p, tid, NT);
+// one launch's shape, shared by host and device through the kernel arguments
+struct StackPlan {
+  int rows, cols, tokens, ngroups;
+  int64_t rbytes, mat_bytes;
+  int items, items_per_mat, rstride, padded, loads, nbuf;  // loads: direct loads a thread an item
+  int rg, kw, nw;                                          // row groups, column splits, waves (rg * kw)
+  int ring_off, buf_bytes, red_off;                        // LDS byte offsets and sizes
+};
+
+// Loop-invariant decode constants held in VGPRs: a gfx9 VOP3 instruction takes no literal, so with the masks and
+// the magic in registers each pair of Q2_0 weights is one v_and_or_b32.
+struct DecodeRegs {
+  uint32_t m0, m1, m2, magic;
+};
+__device__ __forceinline__ uint32_t vreg(uint32_t c) {
+  uint32_t r;
+  asm("v_mov_b32 %0, %1" : "=v"(r) : "s"(c));
+  return r;
+}
+template <int KIND, typename MT> __device__ __forceinline__ DecodeRegs decode_regs() {
+  DecodeRegs r;
+  if constexpr (KIND == Q2_0) {
+    r.m0 = vreg(0x00030003u);
+    r.m1 = vreg(0x000C000Cu);
+    r.m2 = vreg(0x00300030u);
+    r.magic = vreg(Magic<MT>::M2);
+  } else {
+    r.m0 = r.m1 = r.m2 = 0;
+    r.magic = vreg(Magic<MT>::HI * 0x01010101u);
+  }
+  return r;
+}
+
+// a wave's activation fragments for its GPER scale groups (A operand: lane (g, n) holds row n = its token's
+// fragment g), and minus the offsets' sums for the TPG tokens of its D-rows
+template <int KIND, int TPG, int GPER> struct XRegs {
+  u32x4 xa[GPER];
+  u32x4 xb[KIND == Q2_0 ? GPER : 1];
+  float nc[GPER][TPG];
+};
+
+// XRegs for scale groups [gbase, gbase + GPER) of the matrix whose activations start at xm (row t at xm + t * cols).
+// Q2_0: lane g's fragment a takes block-local weights k = 32h + 8g + 4a + j (j < 4, h < 2) into slot 2j + h, scaled
+// by 1 / U_j (the in-place mask's unit), as XStage stages them; IQ3_S: values 8g..8g+7 of the run as they are. The
+// sums: each lane's share, added over the four lanes of a row (xor 16, 32), then fetched from a lane whose A-row is
+// the wanted token (lane 4g + t holds token g * TPG + t). Padding A-rows read token 0.
+template <int KIND, typename XT, int TPG, int GPER>
+__device__ __forceinline__ void load_x(XRegs<KIND, TPG, GPER>& X, const XT* xm, int cols, int n_tok, int gbase) {
+  using MT = XT;
+  const int lane = threadIdx.x & 63, g = lane >> 4;
+  int mt = lane_token<TPG>();
+  mt = mt < n_tok ? mt : 0;
+  const XT* xr = xm + (size_t)mt * cols;
+  float part[GPER];
+  if constexpr (KIND == Q2_0) {
+    u32x4 v[GPER][2];
+#pragma unroll
+    for (int j = 0; j < GPER; ++j) {
+      v[j][0] = *(const u32x4*)(xr + (gbase + j) * 64 + 8 * g);
+      v[j][1] = *(const u32x4*)(xr + (gbase + j) * 64 + 32 + 8 * g);
     }
-    for (int p = 1; p < xst.passes(NT); ++p) {
-      xst.load(p, tid, NT);
-      xst.store(p, tid, NT);
+#pragma unroll
+    for (int j = 0; j < GPER; ++j) {
+      const XT* h0 = (const XT*)&v[j][0];
+      const XT* h1 = (const XT*)&v[j][1];
+      float p = 0.0f;
+      uint32_t w[2][4];
+#pragma unroll
+      for (int a = 0; a < 2; ++a)
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) {
+          const float inv = 1.0f / q2_unit<MT>(jj);  // a power of two: exact
+          const MT s0 = from_f32<MT>(to_f32(h0[4 * a + jj]) * inv);
+          const MT s1 = from_f32<MT>(to_f32(h1[4 * a + jj]) * inv);
+          p += (Magic<MT>::BASE + q2_unit<MT>(jj)) * (to_f32(s0) + to_f32(s1));
+          w[a][jj] = (uint32_t)__builtin_bit_cast(uint16_t, s0) | ((uint32_t)__builtin_bit_cast(uint16_t, s1) << 16);
+        }
+      X.xa[j] = u32x4{w[0][0], w[0][1], w[0][2], w[0][3]};
+      X.xb[j] = u32x4{w[1][0], w[1][1], w[1][2], w[1][3]};
+      part[j] = p;
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < GPER; ++j) X.xa[j] = *(const u32x4*)(xr + (gbase + j) * 32 + 8 * g);
+#pragma unroll
+    for (int j = 0; j < GPER; ++j) {
+      const XT* e = (const XT*)&X.xa[j];
+      float p = 0.0f;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) p += to_f32(e[i]);
+      part[j] = (Magic<MT>::BASE + 16.0f) * p;
     }
   }
-  __syncthreads();
-  for (int item = first; item < last; ++item) {
-    const bool more = item + 1 < last;
-    int nb_next = 0;
-    const uint8_t* src_next = more ? src_of(item + 1, nb_next) : src;
-    const int m_next = more ? (item + 1) / items_per_mat : m;
-    ByteStage<UW> nw(wt, src_next, nb_next, nullptr, nullptr, 0);
-    XStageCorr<KIND, XT, MT, UX> nxs(xs, corr, x + (int64_t)m_next * tokens * cols, m_next != m ? tokens : 0, cols);
-    const bool w1 = nw.passes(NT) <= 1, x1 = nxs.passes(NT) <= 1;
-    if (w1) nw.load(0, tid, NT);  // in flight while this item multiplies
-    if (x1) nxs.load(0, tid, NT);
-
-    const int r0 = (item - m * items_per_mat) * IR;
-    const int rows_here = min(IR, rows - r0);
-    float acc[TPG];
 #pragma unroll
-    for (int t = 0; t < TPG; ++t) acc[t] = 0.0f;
-    if (rg * 16 < rows_here)
-      tile_mac_lds<KIND, MT, TPG>(wt + lead_of(src) + (size_t)rg * 16 * rbytes, (int)rbytes, xs, corr, cols, ngroups,
-                                  tokens, kh * gper, (kh + 1) * gper, (const uint32_t*)tab, acc);
-    if constexpr (KW > 1) {
+  for (int j = 0; j < GPER; ++j) {
+    float p = part[j];
+    p += __shfl_xor(p, 16);
+    p += __shfl_xor(p, 32);
 #pragma unroll
-      for (int t = 0; t < TPG; ++t) s_red[kh][rg][lane][t] = acc[t];
-    }
-    __syncthreads();  // every wave is done with this item's bytes (and has left its partial sums)
-    if (kh == 0 && rg * 16 < rows_here) {
-      const int g = lane >> 4, n = lane & 15;
-#pragma unroll
-      for (int t = 0; t < TPG; ++t) {
-        float total = acc[t];
-        if constexpr (KW > 1) {
-#pragma unroll
-          for (int k2 = 1; k2 < KW; ++k2) total += s_red[k2][rg][lane][t];
-        }
-        const int tok = g * TPG + t, row = r0 + rg * 16 + n;
-        if (tok < tokens && row < rows) out[((int64_t)m * tokens + tok) * rows + row] = from_f32<XT>(total);
-      }
-    }
-    if (more) {
-      if (w1) {
-        nw.store(0, tid, NT);
-      } else {
-        for (int p = 0; p < nw.passes(NT); ++p) {
-          nw.load(p, tid, NT);
-          nw.store(p, tid, NT);
-        }
-      }
-      if (x1) {
-        nxs.store(0, tid, NT);
-      } else {
-        for (int p = 0; p < nxs.passes(NT); ++p) {
-          nxs.load(p, tid, NT);
-          nxs.store(p, tid, NT);
-        }
-      }
-    }
-    src = src_next;
-    m = m_next;
-    __syncthreads();
+    for (int t = 0; t < TPG; ++t) X.nc[j][t] = -__shfl(p, 4 * g + t);
   }
 }
 
-// launch shapes: waves a block, waves splitting the columns, 16-byte weight loads a thread, activation vectors a thread
-template <int KIND, bool STREAM, int TPG> struct StackShape;
-template <int TPG> struct StackShape<Q2_0, true, TPG> { static constexpr int WAVES = 4, KW = 1, UW = 10, UX = 4 * TPG; };
-template <int TPG> struct StackShape<Q2_0, false, TPG> { static constexpr int WAVES = 4, KW = 4, UW = 3, UX = 4 * TPG; };
-template <int TPG> struct StackShape<IQ3_S, true, TPG> { static constexpr int WAVES = 8, KW = 2, UW = 8, UX = 2 * TPG; };
-template <int TPG> struct StackShape<IQ3_S, false, TPG> { static constexpr int WAVES = 4, KW = 4, UW = 4, UX = 4 * TPG; };
+// one wave's item: its 16 rows (row n at wrow0 + n * rstride, already advanced to the wave's first group) x its
+// GPER groups. All LDS reads are issued up front; a group's scale is applied to its accumulator chain (two
+// chains, in turn) after the other chain's MFMAs. The D-rows past TPG are padding rows: their accumulators keep
+// whatever the chain left and are never used.
+template <int KIND, typename MT, int TPG, int GPER>
+__device__ __forceinline__ void item_mac(const uint8_t* wrow0, int rstride, const XRegs<KIND, TPG, GPER>& X,
+                                         const uint32_t* stab, const DecodeRegs& k, float* acc) {
+  const int lane = threadIdx.x & 63, g = lane >> 4, n = lane & 15;
+  const uint8_t* wrow = wrow0 + (size_t)n * rstride;
+  uint32_t w0[GPER], w1[GPER], dh[GPER], sc[GPER];
+  if constexpr (KIND == Q2_0) {
+#pragma unroll
+    for (int j = 0; j < GPER; ++j) {
+      const uint8_t* b = wrow + j * 18;
+      w0[j] = *(const uint16_t*)(b + 2 + 2 * g);
+      w1[j] = *(const uint16_t*)(b + 10 + 2 * g);
+      dh[j] = *(const uint16_t*)b;
+    }
+  } else {
+    uint32_t q2[GPER], qh[GPER], sg[GPER];
+#pragma unroll
+    for (int j = 0; j < GPER; ++j) {
+      const uint8_t* b = wrow + (j >> 3) * 110;
+      const int ib = j & 7;
+      q2[j] = *(const uint16_t*)(b + 2 + 8 * ib + 2 * g);
+      qh[j] = b[66 + ib];
+      sg[j] = b[74 + 4 * ib + g];
+      if (ib % 2 == 0) sc[j] = b[106 + ib / 2];
+      if (ib == 0) dh[j] = *(const uint16_t*)b;
+    }
+#pragma unroll
+    for (int j = 0; j < GPER; ++j) {
+      const uint32_t h = qh[j] >> (2 * g);
+      w0[j] = stab[(q2[j] & 0xffu) | ((h & 1u) << 8) | ((sg[j] & 15u) << 9)];
+      w1[j] = stab[(q2[j] >> 8) | ((h & 2u) << 7) | ((sg[j] >> 4) << 9)];
+    }
+  }
+  f32x4 D[2] = {{0.0f, 0.0f, 0.0f, 0.0f}, {0.0f, 0.0f, 0.0f, 0.0f}};
+  float dprev = 0.0f;
+#pragma unroll
+  for (int j = 0; j < GPER; ++j) {
+    f32x4& Dj = D[j & 1];
+#pragma unroll
+    for (int t = 0; t < TPG; ++t) Dj[t] = X.nc[j][t];
+    if constexpr (KIND == Q2_0) {
+      const uint32_t W = w0[j] | (w1[j] << 16), W8 = W >> 8;
+      u32x4 fa, fb;
+      fa.x = (W & k.m0) | k.magic;
+      fa.y = (W & k.m1) | k.magic;
+      fa.z = (W & k.m2) | k.magic;
+      fb.x = (W8 & k.m0) | k.magic;
+      fb.y = (W8 & k.m1) | k.magic;
+      fb.z = (W8 & k.m2) | k.magic;
+      if constexpr (std::is_same_v<MT, bf16>) {  // bit 7 of a bf16 half is exponent: code 3 shifted down
+        fa.w = ((W >> 6) & k.m0) | k.magic;
+        fb.w = ((W >> 14) & k.m0) | k.magic;
+      } else {
+        fa.w = (W & (k.m2 << 2)) | k.magic;
+        fb.w = (W8 & (k.m2 << 2)) | k.magic;
+      }
+      Dj = mfma<MT>(X.xa[j], fa, Dj);
+      Dj = mfma<MT>(X.xb[j], fb, Dj);
+    } else {
+      u32x4 fw;
+      fw.x = __builtin_amdgcn_perm(k.magic, w0[j], 0x04010400u);
+      fw.y = __builtin_amdgcn_perm(k.magic, w0[j], 0x04030402u);
+      fw.z = __builtin_amdgcn_perm(k.magic, w1[j], 0x04010400u);
+      fw.w = __builtin_amdgcn_perm(k.magic, w1[j], 0x04030402u);
+      Dj = mfma<MT>(X.xa[j], fw, Dj);
+    }
+    if (j > 0) {  // the previous group, on the other chain
+#pragma unroll
+      for (int t = 0; t < TPG; ++t) acc[t] = fmaf(dprev, D[(j - 1) & 1][t], acc[t]);
+    }
+    if constexpr (KIND == Q2_0) {
+      dprev = half_bits(dh[j]);
+    } else {
+      const int ib = j & 7;
+      dprev = half_bits(dh[j & ~7]) * (float)(1 + 2 * ((sc[j & ~1] >> (4 * (ib & 1))) & 15u));
+    }
+  }
+#pragma unroll
+  for (int t = 0; t < TPG; ++t) acc[t] = fmaf(dprev, D[(GPER - 1) & 1][t], acc[t]);
+}
+
+template <int KIND, typename XT, int TPG, int GPER, int NWMAX>
+__global__ __launch_bounds__(NWMAX * 64) void k_stack_mv(const uint8_t* __restrict__ blocks, StackPlan P,
+                                                        const XT* __restrict__ x, XT* __restrict__ out,
+                                                        const uint8_t* __restrict__ signed_tab) {
+  using MT = XT;
+  extern __shared__ u32x4 dyn[];
+  uint8_t* lds = (uint8_t*)dyn;
+  const uint32_t lds_base = SH_LDS_ADDR(dyn);
+  float* red = (float*)(lds + P.red_off);  // [kw - 1][rg][64][TPG]: the column splits' partial sums
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int rg = wave % P.rg, kh = wave / P.rg;
+  const int nt = 64 * P.nw, IR = 16 * P.rg;
+  const int wcol = KIND == Q2_0 ? kh * GPER * 18 : (kh * GPER / 8) * 110;  // the wave's first group in a row
+
+  const int per = (P.items + gridDim.x - 1) / gridDim.x;
+  const int first = blockIdx.x * per, last = min(P.items, first + per);
+  if (first >= last) return;
+
+  // this thread's slot of each of its loads, as a byte offset from the item's first byte (padded layout) or
+  // from the 16-byte chunk holding it (packed layout); clamped to the item's last chunk at issue
+  int pre[STACK_LMAX];
+  const int cpr = P.rstride >> 4, cpr_src = (int)(P.rbytes >> 4);
+#pragma unroll
+  for (int j = 0; j < STACK_LMAX; ++j) {
+    const int s = (j * P.nw + wave) * 64 + lane;
+    if (P.padded) {
+      const int row = s / cpr, kk = s - row * cpr;
+      pre[j] = row * (int)P.rbytes + 16 * min(kk, cpr_src - 1);
+    } else {
+      pre[j] = 16 * s;
+    }
+  }
+  auto src_of = [&](int item) {
+    const int m = item / P.items_per_mat, r0 = (item - m * P.items_per_mat) * IR;
+    return blocks + (int64_t)m * P.mat_bytes + (int64_t)r0 * P.rbytes;
+  };
+  auto issue = [&](int item) {
+    const int m = item / P.items_per_mat, r0 = (item - m * P.items_per_mat) * IR;
+    const int nb = min(IR, P.rows - r0) * (int)P.rbytes;
+    const uint8_t* src = src_of(item);
+    const uint8_t* base = P.padded ? src : (const uint8_t*)((uintptr_t)src & ~(uintptr_t)15);
+    const int lastc = P.padded ? nb - 16 : ((lead_of(src) + nb - 1) & ~15);
+    const uint32_t buf = lds_base + P.ring_off + (item % P.nbuf) * P.buf_bytes + wave * 1024;
+#pragma unroll
+    for (int j = 0; j < STACK_LMAX; ++j)
+      if (j < P.loads) lds_dma16(base, min(pre[j], lastc), buf + j * (nt * 16));
+  };
+
+  // the IQ3_S table (whole waves of 64 chunks; a last wave's chunks past the table repeat its last chunk into
+  // the ring's first bytes, before the ring is filled), then the ring's first NBUF - 1 items
+  if constexpr (KIND == IQ3_S) {
+    constexpr int CH = IQ3S_SIGNED_BYTES / 16;
+    for (int c0 = wave * 64; c0 < CH; c0 += nt) lds_dma16(signed_tab, 16 * min(c0 + lane, CH - 1), lds_base + 16 * c0);
+    wait_vmcnt(0);
+  }
+  for (int k = 0; k < P.nbuf - 1 && first + k < last; ++k) issue(first + k);
+
+  const DecodeRegs kr = decode_regs<KIND, MT>();
+  XRegs<KIND, TPG, GPER> X;
+  // an item's results are stored at the start of the next item, before its loads are issued: a store counts on
+  // vmcnt like a load, and issued after an item's loads it would make the wait for the item before them wait for
+  // part of them too
+  float total[TPG];
+  int64_t out_at = -1;  // the element of the last item's results for this lane's first token, or -1: none
+  auto store_out = [&]() {
+    if (out_at >= 0) {
+      const int g = lane >> 4;
+#pragma unroll
+      for (int t = 0; t < TPG; ++t)
+        if (g * TPG + t < P.tokens) out[out_at + (int64_t)t * P.rows] = from_f32<XT>(total[t]);
+    }
+  };
+  int m = -1;
+  for (int item = first; item < last; ++item) {
+    const int ahead = min(P.nbuf - 2, last - 1 - item);  // items issued after this one
+    wait_vmcnt(ahead * P.loads);
+    lds_sync();  // this item is in LDS for every wave; every wave is done with the item before
+    store_out();
+    if (item + P.nbuf - 1 < last) issue(item + P.nbuf - 1);
+    const int mi = item / P.items_per_mat;
+    if (mi != m) {  // a new matrix: this wave's activation fragments and offset sums
+      m = mi;
+      load_x<KIND, XT, TPG, GPER>(X, x + (int64_t)m * P.tokens * P.cols, P.cols, P.tokens, kh * GPER);
+    }
+    const int r0 = (item - m * P.items_per_mat) * IR;
+    const int rows_here = min(IR, P.rows - r0);
+    float acc[TPG];
+#pragma unroll
+    for (int t = 0; t < TPG; ++t) acc[t] = 0.0f;
+    const uint8_t* row0 = lds + P.ring_off + (item % P.nbuf) * P.buf_bytes + (P.padded ? 0 : lead_of(src_of(item)));
+    if (rg * 16 < rows_here) {
+      // nothing of the LDS / scalar-load counter pending (scalar loads return out of order: with one pending the
+      // multiply's reads could only be waited for all at once)
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      item_mac<KIND, MT, TPG, GPER>(row0 + (size_t)rg * 16 * P.rstride + wcol, P.rstride, X, (const uint32_t*)lds,
+                                    kr, acc);
+    }
+    if (P.kw > 1) {
+      if (kh > 0) {
+#pragma unroll
+        for (int t = 0; t < TPG; ++t) red[(((kh - 1) * P.rg + rg) * 64 + lane) * TPG + t] = acc[t];
+      }
+      lds_sync();
+    }
+    out_at = -1;
+    const int row = r0 + rg * 16 + (lane & 15);
+    if (kh == 0 && rg * 16 < rows_here && row < P.rows) {
+#pragma unroll
+      for (int t = 0; t < TPG; ++t) {
+        total[t] = acc[t];
+        for (int k2 = 1; k2 < P.kw; ++k2) total[t] += red[(((k2 - 1) * P.rg + rg) * 64 + lane) * TPG + t];
+      }
+      out_at = ((int64_t)m * P.tokens + (lane >> 4) * TPG) * P.rows + row;
+    }
+  }
+  store_out();
+  wait_vmcnt(0);
+}
 
 static int device_cus() {
   static int cus = 0;
@@ -143,25 +341,66 @@ static int device_cus() {
   return cus;
 }
 
-template <int KIND, bool STREAM, typename XT, int TPG>
+// the LDS row stride of rows of rbytes: padded by 16-byte chunks so 16 consecutive rows start in distinct
+// 4-bank windows of the 64 banks, where the row is whole chunks and the blocks are 16-byte aligned
+static void row_layout(int64_t rbytes, bool aligned, int& rstride, int& padded) {
+  padded = 0;
+  rstride = (int)rbytes;
+  if (rbytes % 16 || !aligned) return;
+  for (int pad = 0; pad <= 48; pad += 16) {
+    const int dw = (int)(rbytes + pad) / 4;
+    bool distinct = true;
+    for (int a = 0; a < 16 && distinct; ++a)
+      for (int b = a + 1; b < 16 && distinct; ++b) distinct = ((a * dw) % 64) / 4 != ((b * dw) % 64) / 4;
+    if (distinct) {
+      rstride = (int)rbytes + pad;
+      padded = 1;
+      return;
+    }
+  }
+  rstride = (int)rbytes + 16;
+  padded = 1;
+}
+
+template <int KIND, typename XT, int TPG, int GPER>
 static int launch_stack(const uint8_t* blocks, const uint8_t* tables, int64_t n_mats, int64_t rows, int64_t cols,
-                        const XT* x, int64_t tokens, XT* out, hipStream_t stream) {
-  using S = StackShape<KIND, STREAM, TPG>;
-  constexpr int IR = 16 * S::WAVES / S::KW;
-  const int64_t rb = row_bytes(KIND, cols);
-  const int64_t ngroups = cols / (KIND == Q2_0 ? 64 : 32);
-  const int64_t items = n_mats * ((rows + IR - 1) / IR);
-  const size_t lds = (size_t)(KIND == IQ3_S ? IQ3S_SIGNED_BYTES : 0) + (size_t)tokens * cols * sizeof(XT) +
-                     (size_t)((tokens * ngroups + 3) & ~3) * 4 + (size_t)IR * rb + 16;
-  if (lds > 160 * 1024) return fail(E_UNSUPPORTED, "stack_matvec: %zu bytes of LDS", lds);
-  auto kern = k_stack_mv<KIND, XT, TPG, S::WAVES, S::KW, S::UW, S::UX>;
-  int per_cu = 0;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, S::WAVES * 64, lds) != hipSuccess || per_cu < 1)
-    per_cu = 1;
-  const int64_t grid = std::min<int64_t>(items, (int64_t)device_cus() * per_cu);
-  hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(S::WAVES * 64), lds, stream, blocks, rows * rb, (int)rows,
-                     (int)cols, rb, x, (int)tokens, out, tables ? tables + TAB_IQ3S_SIGNED : nullptr, (int)items);
-  return check_launch("stack_matvec");
+                        const XT* x, int64_t tokens, XT* out, bool few, hipStream_t stream) {
+  StackPlan P;
+  P.rows = (int)rows;
+  P.cols = (int)cols;
+  P.tokens = (int)tokens;
+  P.ngroups = (int)(cols / scale_group<KIND>());
+  P.kw = P.ngroups / GPER;
+  P.rg = few ? 1 : std::max(1, 8 / P.kw);
+  P.nw = P.rg * P.kw;
+  const int IR = 16 * P.rg, nt = 64 * P.nw;
+  P.rbytes = row_bytes(KIND, cols);
+  P.mat_bytes = rows * P.rbytes;
+  P.items_per_mat = (int)((rows + IR - 1) / IR);
+  P.items = (int)(n_mats * P.items_per_mat);
+  row_layout(P.rbytes, ((uintptr_t)blocks & 15) == 0, P.rstride, P.padded);
+  const int64_t item_bytes = P.padded ? (int64_t)IR * P.rstride : IR * P.rbytes + 15;
+  P.loads = (int)((item_bytes + 16 * nt - 1) / (16 * nt));
+  if (P.loads > STACK_LMAX || P.nw > 16)
+    return fail(E_UNSUPPORTED, "stack_matvec: rows of %lld bytes", (long long)P.rbytes);
+  P.buf_bytes = P.loads * 16 * nt;
+  P.ring_off = KIND == IQ3_S ? IQ3S_SIGNED_BYTES : 0;
+  const size_t red = (size_t)(P.kw - 1) * P.rg * 64 * TPG * 4, tail = 128;
+  const size_t cap = 160 * 1024;
+  P.nbuf = 3;
+  while (P.nbuf > 2 && (size_t)P.ring_off + (size_t)P.nbuf * P.buf_bytes + red + tail > cap) --P.nbuf;
+  P.red_off = P.ring_off + P.nbuf * P.buf_bytes;
+  const size_t lds = (size_t)P.red_off + red + tail;
+  if (lds > cap) return fail(E_UNSUPPORTED, "stack_matvec: %zu bytes of LDS", lds);
+  auto run = [&](auto kern) {
+    int per_cu = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, nt, lds) != hipSuccess || per_cu < 1) per_cu = 1;
+    const int64_t grid = few ? P.items : std::min<int64_t>(P.items, (int64_t)device_cus() * per_cu);
+    hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(nt), lds, stream, blocks, P, x, out,
+                       tables ? tables + TAB_IQ3S_SIGNED : nullptr);
+    return check_launch("stack_matvec");
+  };
+  return P.nw <= 8 ? run(k_stack_mv<KIND, XT, TPG, GPER, 8>) : run(k_stack_mv<KIND, XT, TPG, GPER, 16>);
 }
 
 }  // namespace sh
@@ -181,28 +420,37 @@ int sh_stack_matvec(int kind, const void* blocks, const void* tables, int64_t n_
   if (st) return st;
   if (n_mats <= 0 || tokens <= 0) return OK;
   if (tokens > 16) return fail(E_SHAPE, "stack_matvec: %lld tokens a matrix (at most 16)", (long long)tokens);
-  if (n_mats * ((rows + 15) / 16) > (1ll << 31) - 1)
-    return fail(E_SHAPE, "stack_matvec: %lld matrices too many", (long long)n_mats);
+  if (n_mats * ((rows + 15) / 16) > (1ll << 31) - 1 || rows * row_bytes(kind, cols) > (1ll << 31) - 1)
+    return fail(E_SHAPE, "stack_matvec: %lld matrices of %lld x %lld too many", (long long)n_mats, (long long)rows,
+                (long long)cols);
   if (!mfma_kind_host(kind) || (x_dtype != BF16 && x_dtype != F16) || cols % 256)
     return fail(E_UNSUPPORTED, "stack_matvec: kind %d, dtype %d, %lld columns (Q2_0 / IQ3_S, bf16 / fp16, columns a "
                 "multiple of 256)", kind, x_dtype, (long long)cols);
   if (!blocks || !x || !out || (kind == IQ3_S && !tables)) return fail(E_ARG, "stack_matvec: null pointer");
+  if (((uintptr_t)x & 15) || (tables && ((uintptr_t)tables & 15)))
+    return fail(E_ARG, "stack_matvec: activations and tables must be 16-byte aligned");
+  // a wave's columns: GPER scale groups (8 or 4 Q2_0 blocks, 16 or 8 IQ3_S runs), at most 16 waves across a row
+  const int64_t ngroups = cols / (kind == Q2_0 ? 64 : 32);
+  const int gper = kind == Q2_0 ? (ngroups % 8 == 0 ? 8 : 4) : (ngroups % 16 == 0 ? 16 : 8);
+  if (ngroups / gper > 16)
+    return fail(E_UNSUPPORTED, "stack_matvec: %lld columns (at most %d)", (long long)cols,
+                16 * gper * (kind == Q2_0 ? 64 : 32));
   const int tpg = tokens <= 4 ? 1 : tokens <= 8 ? 2 : 4;
-  // many items to go round: 64-row items streamed; few: 16-row items with the columns split four ways
-  const bool stream_shape = n_mats * ((rows + 63) / 64) >= 2 * (int64_t)device_cus();
+  // few items to go round the CUs: one row group a block, one item a block
+  const int64_t kw = ngroups / gper, ir = 16 * std::max<int64_t>(1, 8 / kw);
+  const bool few = n_mats * ((rows + ir - 1) / ir) < 2 * (int64_t)device_cus();
   return with_half_dtype(x_dtype, [&](auto* tp) {
     using XT = std::remove_pointer_t<decltype(tp)>;
-    auto go = [&](auto kc, auto sc, auto tc) {
-      constexpr int K = decltype(kc)::value, T = decltype(tc)::value;
-      constexpr bool S = decltype(sc)::value != 0;
-      return launch_stack<K, S, XT, T>((const uint8_t*)blocks, (const uint8_t*)tables, n_mats, rows, cols,
-                                       (const XT*)x, tokens, (XT*)out, (hipStream_t)stream);
+    auto go = [&](auto kc, auto gc, auto tc) {
+      constexpr int K = decltype(kc)::value, G = decltype(gc)::value, T = decltype(tc)::value;
+      return launch_stack<K, XT, T, G>((const uint8_t*)blocks, (const uint8_t*)tables, n_mats, rows, cols,
+                                       (const XT*)x, tokens, (XT*)out, few, (hipStream_t)stream);
     };
-    auto by_t = [&](auto kc, auto sc) {
-      return tpg == 1 ? go(kc, sc, kind_c<1>{}) : tpg == 2 ? go(kc, sc, kind_c<2>{}) : go(kc, sc, kind_c<4>{});
+    auto by_t = [&](auto kc, auto gc) {
+      return tpg == 1 ? go(kc, gc, kind_c<1>{}) : tpg == 2 ? go(kc, gc, kind_c<2>{}) : go(kc, gc, kind_c<4>{});
     };
-    auto by_s = [&](auto kc) { return stream_shape ? by_t(kc, kind_c<1>{}) : by_t(kc, kind_c<0>{}); };
-    return kind == Q2_0 ? by_s(kind_c<Q2_0>{}) : by_s(kind_c<IQ3_S>{});
+    if (kind == Q2_0) return gper == 8 ? by_t(kind_c<Q2_0>{}, kind_c<8>{}) : by_t(kind_c<Q2_0>{}, kind_c<4>{});
+    return gper == 16 ? by_t(kind_c<IQ3_S>{}, kind_c<16>{}) : by_t(kind_c<IQ3_S>{}, kind_c<8>{});
   });
 }
 

@@ -103,6 +103,42 @@ constexpr int IQ3S_SIGNED_BYTES = 8192 * 4;  // entry (grid index | sign nibble 
 
 __device__ __forceinline__ int lead_of(const void* p) { return (int)((uintptr_t)p & 15); }
 
+// ---- direct loads into LDS (gfx950 global_load_lds_dwordx4): lane l of the wave writes the 16 bytes at
+// base + off_l to LDS address lds + 16 * l; base and lds (an LDS byte address, lds_addr of the block's LDS array
+// plus an offset) are the same for every lane of the wave. The load counts in vmcnt like
+// any other; readers wait with wait_vmcnt and meet at lds_sync. Issued from inline assembly: the compiler's wait
+// insertion, which would count such a load as pending on the LDS counter too and then wait for every LDS read at
+// once, does not see it (its own waits on younger loads stay correct: the counter drains in order).
+__device__ __forceinline__ void lds_dma16(const void* base, uint32_t off, uint32_t lds) {
+  asm volatile("global_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base), "{m0}"(__builtin_amdgcn_readfirstlane(lds))
+               : "memory");
+}
+// the LDS byte address of a __shared__ array (cast on the array itself: no null check of a generic pointer)
+#define SH_LDS_ADDR(arr) ((uint32_t)(uintptr_t)(__attribute__((address_space(3))) void*)(arr))
+
+// at most n of this wave's memory loads still in flight (n wave-uniform; values above 63 wait for none)
+__device__ __forceinline__ void wait_vmcnt(int n) {
+#define SH_VMCNT_CASE(k) \
+  case k: asm volatile("s_waitcnt vmcnt(" #k ")" ::: "memory"); break;
+#define SH_VMCNT_8(k) SH_VMCNT_CASE(k) SH_VMCNT_CASE(k + 1) SH_VMCNT_CASE(k + 2) SH_VMCNT_CASE(k + 3) \
+  SH_VMCNT_CASE(k + 4) SH_VMCNT_CASE(k + 5) SH_VMCNT_CASE(k + 6) SH_VMCNT_CASE(k + 7)
+  switch (n) {
+    SH_VMCNT_8(0) SH_VMCNT_8(8) SH_VMCNT_8(16) SH_VMCNT_8(24) SH_VMCNT_8(32) SH_VMCNT_8(40) SH_VMCNT_8(48)
+    SH_VMCNT_8(56)
+    default: break;
+  }
+#undef SH_VMCNT_8
+#undef SH_VMCNT_CASE
+}
+
+// every wave's LDS stores done and visible to the block; loads into LDS still in flight stay in flight (a
+// __syncthreads would wait for them)
+__device__ __forceinline__ void lds_sync() {
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
 // Up to two byte ranges to LDS, range i at dst_i + (src_i & 15) (alignment kept modulo 16), 16-byte chunks; edge
 // chunks byte by byte. A pass covers UNROLL * nthreads chunks: load(pass) then store(pass).
 template <int UNROLL> struct ByteStage {
@@ -237,8 +273,8 @@ template <int TPG> __device__ __forceinline__ int lane_token() {
   return (n & 3) < TPG ? (n >> 2) * TPG + (n & 3) : 4 * TPG;
 }
 
-// XStage that also leaves, per scale group of each row, the sum the magic-number decode's constant offsets add
-// (Q2_0: sum_k (BASE + U_k) xs_k; IQ3_S: sum_k (BASE + 16) x_k) at corr[t * ngroups + group]: the eight (Q2_0) or
+// XStage that also leaves, per scale group of each row, minus the sum the magic-number decode's constant offsets
+// add (Q2_0: sum_k (BASE + U_k) xs_k; IQ3_S: sum_k (BASE + 16) x_k) at corr[t * ngroups + group]: the eight (Q2_0) or
 // four (IQ3_S) threads of a group hold consecutive vectors and meet by __shfl_xor. nthreads % 64 == 0.
 template <int KIND, typename XT, typename MT, int UNROLL> struct XStageCorr {
   static_assert(sizeof(XT) == 2, "16-bit activations");
@@ -290,67 +326,11 @@ template <int KIND, typename XT, typename MT, int UNROLL> struct XStageCorr {
       for (int o = LANES >> 1; o > 0; o >>= 1) part += __shfl_xor(part, o);
       if (i < total && (tid & (LANES - 1)) == 0) {
         const int t = i / per_row, c8 = i - t * per_row;
-        corr[t * (cols / SG) + (8 * c8) / SG] = part;
+        corr[t * (cols / SG) + (8 * c8) / SG] = -part;
       }
     }
   }
 };
-
-// One wave's 16-row tile x [g_begin, g_end) scale groups against activations staged in LDS by XStageCorr: the
-// accumulator starts at minus the offsets' sum of its token, so a Q2_0 block takes 2 MFMAs and an IQ3_S run 1.
-// Fragments and sums are read from LDS a scale group at a time.
-template <int KIND, typename MT, int TPG>
-__device__ __forceinline__ void tile_mac_lds(const uint8_t* wrow0, int rbytes, const MT* xs, const float* corr,
-                                             int cols, int ngroups, int n_tok, int g_begin, int g_end,
-                                             const uint32_t* stab, float* acc) {
-  const int lane = threadIdx.x & 63, g = lane >> 4, n = lane & 15;
-  const int mt = lane_token<TPG>();
-  const bool areal = mt < n_tok;
-  const uint8_t* wrow = wrow0 + (size_t)n * rbytes;
-  const MT* xt = xs + (size_t)(areal ? mt : 0) * cols;
-  const u32x4 zfrag = {0u, 0u, 0u, 0u};
-  bool dreal[TPG];
-#pragma unroll
-  for (int t = 0; t < TPG; ++t) dreal[t] = g * TPG + t < n_tok;
-  for (int sg = g_begin; sg < g_end; ++sg) {
-    f32x4 C = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-    for (int t = 0; t < TPG; ++t)
-      if (dreal[t]) C[t] = -corr[(g * TPG + t) * ngroups + sg];
-    if constexpr (KIND == Q2_0) {
-      const uint8_t* b = wrow + sg * 18;
-      const uint32_t W = (uint32_t)*(const uint16_t*)(b + 2 + 2 * g) | ((uint32_t)*(const uint16_t*)(b + 10 + 2 * g) << 16);
-      const float d = half_bits(*(const uint16_t*)b);
-      u32x4 fa, fb;
-      q2_decode<MT>(W, fa, fb);
-      const u32x4 xa = areal ? *(const u32x4*)(xt + sg * 64 + g * 8) : zfrag;
-      const u32x4 xb = areal ? *(const u32x4*)(xt + sg * 64 + 32 + g * 8) : zfrag;
-      f32x4 D = mfma<MT>(xa, fa, C);
-      D = mfma<MT>(xb, fb, D);
-#pragma unroll
-      for (int t = 0; t < TPG; ++t) acc[t] = fmaf(d, D[t], acc[t]);
-    } else {
-      constexpr uint32_t hi4 = Magic<MT>::HI * 0x01010101u;
-      const uint8_t* b = wrow + (sg >> 3) * 110;
-      const int ib = sg & 7;
-      const float db = half_bits(*(const uint16_t*)b) * (float)(1 + 2 * (((uint32_t)b[106 + ib / 2] >> (4 * (ib & 1))) & 15u));
-      const uint32_t q2 = *(const uint16_t*)(b + 2 + 8 * ib + 2 * g);
-      const uint32_t qh = (uint32_t)b[66 + ib] >> (2 * g);
-      const uint32_t sgn = b[74 + 4 * ib + g];
-      const uint32_t e0 = stab[(q2 & 0xffu) | ((qh & 1u) << 8) | ((sgn & 15u) << 9)];
-      const uint32_t e1 = stab[(q2 >> 8) | ((qh & 2u) << 7) | ((sgn >> 4) << 9)];
-      u32x4 fw;
-      fw.x = __builtin_amdgcn_perm(hi4, e0, 0x04010400u);
-      fw.y = __builtin_amdgcn_perm(hi4, e0, 0x04030402u);
-      fw.z = __builtin_amdgcn_perm(hi4, e1, 0x04010400u);
-      fw.w = __builtin_amdgcn_perm(hi4, e1, 0x04030402u);
-      const u32x4 xa = areal ? *(const u32x4*)(xt + sg * 32 + g * 8) : zfrag;
-      const f32x4 D = mfma<MT>(xa, fw, C);
-#pragma unroll
-      for (int t = 0; t < TPG; ++t) acc[t] = fmaf(db, D[t], acc[t]);
-    }
-  }
-}
 
 // ---- the tile multiply-accumulate: this wave's share of a 16-row tile's columns, for the block's tokens
 //
