@@ -150,6 +150,27 @@ int sh_moe_decode_phase(int phase, int kind, int kind_down, const void* gate, co
                         const void* x, int dtype, int64_t tokens, int64_t k, int64_t d_model, int64_t d_ff, void* out,
                         void* workspace, size_t workspace_bytes, void* stream);
 
+/* ---- decode attention (strata_mlx/attention.py:118-165) */
+
+/* _gathered over a page table (attention.py:144-165 with cells = page_table[p / 16] * 16 + p % 16): q (n_q, hq,
+ * head_dim), k_pages / v_pages (n_pages, hkv, 16, head_dim), page_table int32 (ceil(ctx_len / 16)) of physical
+ * pages; the n_q queries are the last positions of the context and query t sees positions <= ctx_len - n_q + t
+ * (the causal mask among a window's drafts, attention.py:118-129). out (n_q, hq, head_dim) in `dtype` (bf16 or
+ * fp16, the dtype of q, k and v); scores and sums in fp32. head_dim 128 or 256. workspace:
+ * sh_paged_attn_workspace() bytes (the splits of the context). */
+size_t sh_paged_attn_workspace(int64_t n_q, int64_t hq, int64_t hkv, int64_t head_dim, int64_t ctx_len);
+int sh_paged_attn(const void* q, const void* k_pages, const void* v_pages, const int32_t* page_table, int64_t n_pages,
+                  int64_t ctx_len, int64_t n_q, int64_t hq, int64_t hkv, int64_t head_dim, float scale, int dtype,
+                  void* out, void* workspace, size_t workspace_bytes, void* stream);
+
+/* _gathered in its own form (attention.py:132-165): query s attends to the n_cells cells cells[s] (int32, rows of
+ * k / v (hkv, kv_len, head_dim)) whose flag real[s] (uint8) is set; q (n_q, hq, head_dim) -> out (n_q, hq,
+ * head_dim). workspace: sh_cells_attn_workspace() bytes. */
+size_t sh_cells_attn_workspace(int64_t n_q, int64_t hq, int64_t hkv, int64_t head_dim, int64_t n_cells);
+int sh_cells_attn(const void* q, const void* k, const void* v, int64_t kv_len, const int32_t* cells,
+                  const uint8_t* real, int64_t n_cells, int64_t n_q, int64_t hq, int64_t hkv, int64_t head_dim,
+                  float scale, int dtype, void* out, void* workspace, size_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

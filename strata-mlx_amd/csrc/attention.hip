@@ -1,0 +1,417 @@
+// Decode attention over a paged KV cache, split over the context, GQA: the query heads that share a KV head are
+// that head's query rows — strata-mlx's `_gathered` (strata_mlx/attention.py:144-165), which attends each query to
+// its cell list with the group of query heads as the rows of one SDPA, taken to a page table: position p of the
+// context is cell table[p / 16] * 16 + p % 16. The window's B queries are the last B positions; query t sees
+// positions 0 .. ctx - B + t (the causal mask among drafts, attention.py:118-129). The same kernel also takes
+// `_gathered`'s own form: a list of cells per query, each with a validity flag (attention.py:132-141).
+//
+// Split-K: block (split, unit, row group) runs the online softmax over its run of 16-position tiles for up to 64
+// query rows and leaves (max, sum, unnormalised output) in a workspace; a second kernel merges the splits.
+//
+// Per tile, on MFMA (16x16x32 bf16/f16 for scores, 16x16x16 for the values):
+//   S^T = K Q^T: K (16 positions x D) is the A operand read from LDS, Q^T the B operand held in registers, so a
+//        lane (g, n) holds the scores of positions 4g..4g+3 for query row n;
+//   O += P V:    that is exactly the A operand layout of P for 16x16x16 (row n, positions 4g..4g+3); V (16 x D)
+//        is the B operand, read from LDS; O[row 4g + i][dim n] accumulates in registers, 16 dims a tile.
+// The block's tiles come into LDS by direct 16-byte loads (no registers), two steps of tiles in flight; rows of K
+// and V sit at a 528-byte stride (33 chunks), so the 16 positions a read touches fall in distinct banks.
+#include <type_traits>
+
+#include "launch.h"
+#include "xmv.h"
+
+namespace sh {
+
+struct AttnArgs {
+  const void* q;             // (n_q, hq, D)
+  const void* k;             // paged: (pages, hkv, 16, D); cells: (hkv, kv_len, D)
+  const void* v;
+  const int32_t* table;      // paged: physical page of each tile of 16 positions; cells: (n_q, ctx) cell ids
+  const uint8_t* real;       // cells: (n_q, ctx) validity; paged: null
+  float* ws;                 // [splits][units][rows][D + 2]: max, sum, output
+  void* out;                 // (n_q, hq, D)
+  int n_q, hq, hkv, ctx;     // ctx: paged context length, or cells a query
+  int64_t kv_len;            // cells: rows of one KV head
+  int tiles, tiles_per_split, splits, units, rows;  // rows: query rows of a unit (paged n_q * group, cells group)
+  float scale_log2;          // scale * log2(e)
+};
+
+constexpr int ATT_WAVES = 4, ATT_NT = 256;
+template <int D> constexpr int att_part_slots() { return 16 * (D / 8 + 1); }  // a tile's K or V, padded rows
+template <int D> constexpr int att_part_insts() { return (att_part_slots<D>() + 63) / 64; }
+template <int D> constexpr int att_part_bytes() { return att_part_insts<D>() * 64 * 16; }
+
+template <typename XT> __device__ __forceinline__ f32x4 mfma16x16x16(uint32_t a0, uint32_t a1, uint32_t b0, uint32_t b1,
+                                                                     f32x4 c) {
+  typedef short s4 __attribute__((ext_vector_type(4)));
+  typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+  const uint64_t a = (uint64_t)a0 | ((uint64_t)a1 << 32), b = (uint64_t)b0 | ((uint64_t)b1 << 32);
+  if constexpr (std::is_same_v<XT, bf16>)
+    return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(s4, a), __builtin_bit_cast(s4, b), c, 0, 0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(h4, a), __builtin_bit_cast(h4, b), c, 0, 0, 0);
+}
+
+template <typename XT> __device__ __forceinline__ uint32_t pack_pair(float lo, float hi) {
+  return (uint32_t)__builtin_bit_cast(uint16_t, from_f32<XT>(lo)) |
+         ((uint32_t)__builtin_bit_cast(uint16_t, from_f32<XT>(hi)) << 16);
+}
+
+// Block: 4 waves; RT4 row tiles of 16 rows (1, 2 or 4) x PL = 4 / RT4 tile phases. A step stages PL tiles; wave
+// (rt, ph) multiplies row tile rt against the step's tile ph.
+template <typename XT, int D, bool CELLS>
+__global__ __launch_bounds__(ATT_NT) void k_attn_split(AttnArgs a) {
+  constexpr int NC = D / 32, NDT = D / 16, PS = att_part_slots<D>(), PI = att_part_insts<D>();
+  constexpr int PB = att_part_bytes<D>(), RS = (D / 8 + 1) * 16;  // bytes a staged row
+  extern __shared__ u32x4 dyn[];
+  const uint32_t lds_base = SH_LDS_ADDR(dyn);
+  const uint8_t* lds = (const uint8_t*)dyn;
+  const int lane = threadIdx.x & 63, g = lane >> 4, n = lane & 15;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int split = blockIdx.x, unit = blockIdx.y, zrow = blockIdx.z * 64;
+  const int group = a.hq / a.hkv;
+  const int h = CELLS ? unit % a.hkv : unit;
+  const int qcell = CELLS ? unit / a.hkv : 0;  // cells form: the unit's one query
+  const int rows_here = min(64, a.rows - zrow);
+  const int RT = (rows_here + 15) / 16, RT4 = RT <= 1 ? 1 : RT <= 2 ? 2 : 4, PL = ATT_WAVES / RT4;
+  const int rt = wave % RT4, ph = wave / RT4;
+  const int t0 = split * a.tiles_per_split, t1 = min(a.tiles, t0 + a.tiles_per_split);
+  const int steps = (t1 - t0 + PL - 1) / PL;
+  const int step_bytes = 2 * PL * PB;  // K and V of PL tiles
+
+  // ---- this wave's direct loads of a step: instruction q of the step's 2 * PL * PI is wave q % 4's
+  const int n_inst = 2 * PL * PI;
+  const int my_insts = (n_inst - wave + ATT_WAVES - 1) / ATT_WAVES;
+  const XT* kb = (const XT*)a.k;
+  const XT* vb = (const XT*)a.v;
+  auto row_off = [&](int tile, int tok) -> int64_t {  // elements from the K / V base to a tile position's row
+    if constexpr (CELLS) {
+      const int pos = min(tile * 16 + tok, a.ctx - 1);
+      const int cell = a.table[(int64_t)qcell * a.ctx + pos];
+      return ((int64_t)h * a.kv_len + cell) * D;
+    } else {
+      const int64_t phys = a.table[min(tile, a.tiles - 1)];
+      return ((phys * a.hkv + h) * 16 + tok) * D;
+    }
+  };
+  auto issue = [&](int step) {
+    const uint32_t buf = lds_base + (step & 1) * step_bytes;
+    for (int q = wave; q < n_inst; q += ATT_WAVES) {
+      const int part = q / PI, j = q - part * PI;  // part: tile ph' = part / 2, K (0) or V (1)
+      const int tile = min(t0 + step * PL + part / 2, t1 - 1);
+      const int s = j * 64 + lane;
+      const int tok = min(s / (D / 8 + 1), 15);
+      const int piece = min(s - (s / (D / 8 + 1)) * (D / 8 + 1), D / 8 - 1);
+      const int64_t off = (row_off(tile, tok) + 8 * piece) * (int64_t)sizeof(XT);
+      lds_dma16(part & 1 ? (const void*)vb : (const void*)kb, (uint32_t)off, buf + part * PB + j * 1024);
+    }
+  };
+
+  // ---- Q^T fragments (B operand of S^T = K Q^T): lane (g, n) holds row n's dims c*32 + 8g .. +7
+  const int r_local = 16 * rt + n;                     // the lane's B column: its query row within the block
+  const int row = zrow + min(r_local, rows_here - 1);  // padding rows repeat the last real one (never stored)
+  const int qt = CELLS ? qcell : row / group, qh = h * group + (CELLS ? row : row % group);
+  const XT* qrow = (const XT*)a.q + ((int64_t)qt * a.hq + qh) * D;
+  u32x4 qf[NC];
+#pragma unroll
+  for (int c = 0; c < NC; ++c) qf[c] = *(const u32x4*)(qrow + c * 32 + 8 * g);
+  // the last position the lane's query row may see (paged: causal among the window's queries)
+  const int vis_last = CELLS ? a.ctx - 1 : a.ctx - a.n_q + qt;
+
+  float m_run = -INFINITY, l_run = 0.0f;  // for query row n (replicated over g)
+  f32x4 O[NDT];
+#pragma unroll
+  for (int dt = 0; dt < NDT; ++dt) O[dt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+
+  if (steps > 0) issue(0);
+  for (int st = 0; st < steps; ++st) {
+    const bool more = st + 1 < steps;
+    if (more) issue(st + 1);
+    wait_vmcnt(more ? my_insts : 0);
+    lds_sync();
+    const int tile = t0 + st * PL + ph;
+    if (rt < RT && tile < t1) {
+      const uint8_t* kt = lds + (st & 1) * step_bytes + (2 * ph) * PB;
+      const uint8_t* vt = kt + PB;
+      // scores of positions 4g..4g+3 for row n
+      f32x4 S = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int c = 0; c < NC; ++c) {
+        const u32x4 kf = *(const u32x4*)(kt + n * RS + c * 64 + 16 * g);
+        S = mfma<XT>(kf, qf[c], S);
+      }
+      float sv[4], mx = -INFINITY;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int pos = tile * 16 + 4 * g + i;
+        bool ok;
+        if constexpr (CELLS) ok = pos < a.ctx && a.real[(int64_t)qcell * a.ctx + pos] != 0;
+        else ok = pos < a.ctx && pos <= vis_last;
+        sv[i] = ok ? S[i] * a.scale_log2 : -INFINITY;
+        mx = fmaxf(mx, sv[i]);
+      }
+      mx = fmaxf(mx, __shfl_xor(mx, 16));
+      mx = fmaxf(mx, __shfl_xor(mx, 32));
+      const float m_new = fmaxf(m_run, mx);
+      const float base = m_new == -INFINITY ? 0.0f : m_new;  // a row with nothing visible yet stays at zero
+      const float alpha = exp2f(m_run - base);
+      float p[4], ps = 0.0f;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        p[i] = exp2f(sv[i] - base);
+        ps += p[i];
+      }
+      ps += __shfl_xor(ps, 16);
+      ps += __shfl_xor(ps, 32);
+      l_run = l_run * alpha + ps;
+      m_run = m_new;
+      // O rows are 4g + i: their factors sit with the lanes whose column is that row
+      if (__any(alpha != 1.0f)) {
+        float ar[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) ar[i] = __shfl(alpha, 4 * g + i);
+#pragma unroll
+        for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) O[dt][i] *= ar[i];
+      }
+      const uint32_t pa0 = pack_pair<XT>(p[0], p[1]), pa1 = pack_pair<XT>(p[2], p[3]);
+#pragma unroll
+      for (int dt = 0; dt < NDT; ++dt) {
+        const uint8_t* vc = vt + (16 * dt + n) * 2;
+        const uint32_t v0 = *(const uint16_t*)(vc + (4 * g + 0) * RS), v1 = *(const uint16_t*)(vc + (4 * g + 1) * RS);
+        const uint32_t v2 = *(const uint16_t*)(vc + (4 * g + 2) * RS), v3 = *(const uint16_t*)(vc + (4 * g + 3) * RS);
+        O[dt] = mfma16x16x16<XT>(pa0, pa1, v0 | (v1 << 16), v2 | (v3 << 16), O[dt]);
+      }
+    }
+    lds_sync();  // every wave is done with this step's buffer before the step after next fills it
+  }
+
+  // ---- merge the PL phases of each row tile in LDS, then the first phase's wave writes the split's partial
+  float* red = (float*)dyn;  // [ph][rt][64 lanes]: m, l, then O [ph][rt][dims][16 rows]
+  float* redo = red + 2 * ATT_WAVES * 64;
+  if (PL > 1) {
+    red[(ph * RT4 + rt) * 64 + lane] = m_run;
+    red[ATT_WAVES * 64 + (ph * RT4 + rt) * 64 + lane] = l_run;
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) redo[((ph * RT4 + rt) * D + 16 * dt + n) * 16 + 4 * g + i] = O[dt][i];
+    lds_sync();
+    if (ph == 0) {
+      // lane (g, n): its column row n for m, l; O rows 4g + i
+      float m_all = m_run;
+      for (int p2 = 1; p2 < PL; ++p2) m_all = fmaxf(m_all, red[(p2 * RT4 + rt) * 64 + lane]);
+      const float base = m_all == -INFINITY ? 0.0f : m_all;
+      float l_all = 0.0f;
+      for (int p2 = 0; p2 < PL; ++p2)
+        l_all += red[ATT_WAVES * 64 + (p2 * RT4 + rt) * 64 + lane] * exp2f(red[(p2 * RT4 + rt) * 64 + lane] - base);
+      float fr[ATT_WAVES][4];
+      for (int p2 = 0; p2 < PL; ++p2)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) fr[p2][i] = exp2f(red[(p2 * RT4 + rt) * 64 + 4 * g + i] - __shfl(base, 4 * g + i));
+#pragma unroll
+      for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          float o = 0.0f;
+          for (int p2 = 0; p2 < PL; ++p2) o += redo[((p2 * RT4 + rt) * D + 16 * dt + n) * 16 + 4 * g + i] * fr[p2][i];
+          O[dt][i] = o;
+        }
+      m_run = m_all;
+      l_run = l_all;
+    }
+  }
+  if (ph == 0 && rt < RT) {
+    float* w = a.ws + ((int64_t)split * a.units + unit) * (int64_t)a.rows * (D + 2);
+    const int r_col = zrow + r_local;  // lane's column row (m, l)
+    if (g == 0 && r_local < rows_here) {
+      w[(int64_t)r_col * (D + 2)] = m_run;
+      w[(int64_t)r_col * (D + 2) + 1] = l_run;
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int rl = 16 * rt + 4 * g + i;
+      if (rl < rows_here) {
+#pragma unroll
+        for (int dt = 0; dt < NDT; ++dt) w[(int64_t)(zrow + rl) * (D + 2) + 2 + 16 * dt + n] = O[dt][i];
+      }
+    }
+  }
+}
+
+// merge the splits of one (unit, row): out = sum_s O_s 2^(m_s - m) / sum_s l_s 2^(m_s - m); a row that sees no
+// position (every cell masked) gives zeros
+template <typename XT, int D, bool CELLS>
+__global__ __launch_bounds__(256) void k_attn_merge(AttnArgs a) {
+  const int unit = blockIdx.y, row = blockIdx.x;
+  const int group = a.hq / a.hkv;
+  const int h = CELLS ? unit % a.hkv : unit;
+  const int qt = CELLS ? unit / a.hkv : row / group, qh = h * group + (CELLS ? row : row % group);
+  const int64_t stride = (int64_t)a.units * a.rows * (D + 2);
+  const float* w0 = a.ws + ((int64_t)unit * a.rows + row) * (D + 2);
+  float m = -INFINITY;
+  for (int s = 0; s < a.splits; ++s) m = fmaxf(m, w0[s * stride]);
+  const float base = m == -INFINITY ? 0.0f : m;
+  float l = 0.0f;
+  for (int s = 0; s < a.splits; ++s) l += w0[s * stride + 1] * exp2f(w0[s * stride] - base);
+  const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+  XT* o = (XT*)a.out + ((int64_t)qt * a.hq + qh) * D;
+  for (int d = threadIdx.x; d < D; d += blockDim.x) {
+    float acc = 0.0f;
+    for (int s = 0; s < a.splits; ++s) acc += w0[s * stride + 2 + d] * exp2f(w0[s * stride] - base);
+    o[d] = from_f32<XT>(acc * inv);
+  }
+}
+
+static int attn_cus() {
+  static int cus = 0;
+  if (!cus) {
+    int dev = 0;
+    (void)hipGetDevice(&dev);
+    (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+    if (cus <= 0) cus = 256;
+  }
+  return cus;
+}
+
+// splits of the context: enough blocks to fill the chip twice over, at least 4 tiles a split
+static void plan_splits(AttnArgs& a, int zgroups) {
+  const int64_t want = 2 * (int64_t)attn_cus();
+  const int64_t per_unit = std::max<int64_t>(1, want / ((int64_t)a.units * zgroups));
+  a.tiles_per_split = (int)std::max<int64_t>(4, (a.tiles + per_unit - 1) / per_unit);
+  a.splits = (a.tiles + a.tiles_per_split - 1) / a.tiles_per_split;
+}
+
+template <int D> static size_t attn_lds(int rows_here) {
+  const int RT = (rows_here + 15) / 16, RT4 = RT <= 1 ? 1 : RT <= 2 ? 2 : 4, PL = ATT_WAVES / RT4;
+  const size_t stage = 2 * (size_t)(2 * PL * att_part_bytes<D>());
+  const size_t merge = sizeof(float) * (2 * ATT_WAVES * 64 + (size_t)ATT_WAVES * D * 16);
+  return std::max(stage, merge);
+}
+
+template <typename XT, int D, bool CELLS> static int launch_attn(AttnArgs a, hipStream_t stream) {
+  const int zgroups = CELLS ? 1 : (a.rows + 63) / 64;
+  plan_splits(a, zgroups);
+  const size_t lds = attn_lds<D>(std::min(64, a.rows));
+  if (lds > 160 * 1024) return fail(E_UNSUPPORTED, "attention: %zu bytes of LDS", lds);
+  hipLaunchKernelGGL((k_attn_split<XT, D, CELLS>), dim3(a.splits, a.units, zgroups), dim3(ATT_NT), lds, stream, a);
+  int st = check_launch("attention split");
+  if (st) return st;
+  hipLaunchKernelGGL((k_attn_merge<XT, D, CELLS>), dim3(a.rows, a.units), dim3(std::min(D, 256)), 0, stream, a);
+  return check_launch("attention merge");
+}
+
+static size_t attn_ws_bytes(int units, int rows, int tiles, int zgroups, int D) {
+  AttnArgs a{};
+  a.units = units;
+  a.tiles = tiles;
+  plan_splits(a, zgroups);
+  return (size_t)a.splits * units * rows * (D + 2) * sizeof(float);
+}
+
+}  // namespace sh
+
+using namespace sh;
+
+extern "C" {
+
+size_t sh_paged_attn_workspace(int64_t n_q, int64_t hq, int64_t hkv, int64_t head_dim, int64_t ctx_len) {
+  if (n_q <= 0 || hkv <= 0 || hq % hkv || ctx_len <= 0) return 0;
+  const int rows = (int)(n_q * (hq / hkv));
+  return attn_ws_bytes((int)hkv, rows, (int)((ctx_len + 15) / 16), (rows + 63) / 64, (int)head_dim);
+}
+
+int sh_paged_attn(const void* q, const void* k_pages, const void* v_pages, const int32_t* page_table, int64_t n_pages,
+                  int64_t ctx_len, int64_t n_q, int64_t hq, int64_t hkv, int64_t head_dim, float scale, int dtype,
+                  void* out, void* workspace, size_t workspace_bytes, void* stream) {
+  if (n_q <= 0) return OK;
+  if (hkv <= 0 || hq <= 0 || hq % hkv) return fail(E_SHAPE, "paged_attn: %lld query heads over %lld KV heads",
+                                                   (long long)hq, (long long)hkv);
+  if (head_dim != 256 && head_dim != 128) return fail(E_UNSUPPORTED, "paged_attn: head_dim %lld (128 or 256)",
+                                                      (long long)head_dim);
+  if (ctx_len <= 0 || n_q > ctx_len) return fail(E_SHAPE, "paged_attn: %lld queries in a context of %lld",
+                                                 (long long)n_q, (long long)ctx_len);
+  if (n_pages < (ctx_len + 15) / 16) return fail(E_SHAPE, "paged_attn: %lld pages for %lld positions",
+                                                 (long long)n_pages, (long long)ctx_len);
+  if (n_pages * hkv * 16 * head_dim * 2 > (int64_t)UINT32_MAX)
+    return fail(E_UNSUPPORTED, "paged_attn: a K or V pool of more than 4 GiB");
+  if (!q || !k_pages || !v_pages || !page_table || !out) return fail(E_ARG, "paged_attn: null pointer");
+  if (((uintptr_t)q | (uintptr_t)k_pages | (uintptr_t)v_pages) & 15)
+    return fail(E_ARG, "paged_attn: q, k and v must be 16-byte aligned");
+  const size_t need = sh_paged_attn_workspace(n_q, hq, hkv, head_dim, ctx_len);
+  if (!workspace || workspace_bytes < need)
+    return fail(E_WORKSPACE, "paged_attn: workspace of %zu bytes, %zu needed", workspace_bytes, need);
+  AttnArgs a{};
+  a.q = q;
+  a.k = k_pages;
+  a.v = v_pages;
+  a.table = page_table;
+  a.real = nullptr;
+  a.ws = (float*)workspace;
+  a.out = out;
+  a.n_q = (int)n_q;
+  a.hq = (int)hq;
+  a.hkv = (int)hkv;
+  a.ctx = (int)ctx_len;
+  a.tiles = (int)((ctx_len + 15) / 16);
+  a.units = (int)hkv;
+  a.rows = (int)(n_q * (hq / hkv));
+  a.scale_log2 = scale * 1.4426950408889634f;
+  return with_half_dtype(dtype, [&](auto* tp) {
+    using XT = std::remove_pointer_t<decltype(tp)>;
+    return head_dim == 256 ? launch_attn<XT, 256, false>(a, (hipStream_t)stream)
+                           : launch_attn<XT, 128, false>(a, (hipStream_t)stream);
+  });
+}
+
+size_t sh_cells_attn_workspace(int64_t n_q, int64_t hq, int64_t hkv, int64_t head_dim, int64_t cells) {
+  if (n_q <= 0 || hkv <= 0 || hq % hkv || cells <= 0) return 0;
+  return attn_ws_bytes((int)(n_q * hkv), (int)(hq / hkv), (int)((cells + 15) / 16), 1, (int)head_dim);
+}
+
+int sh_cells_attn(const void* q, const void* k, const void* v, int64_t kv_len, const int32_t* cells,
+                  const uint8_t* real, int64_t n_cells, int64_t n_q, int64_t hq, int64_t hkv, int64_t head_dim,
+                  float scale, int dtype, void* out, void* workspace, size_t workspace_bytes, void* stream) {
+  if (n_q <= 0) return OK;
+  if (hkv <= 0 || hq <= 0 || hq % hkv) return fail(E_SHAPE, "cells_attn: %lld query heads over %lld KV heads",
+                                                   (long long)hq, (long long)hkv);
+  if (hq / hkv > 64) return fail(E_UNSUPPORTED, "cells_attn: %lld query heads a KV head (at most 64)",
+                                 (long long)(hq / hkv));
+  if (head_dim != 256 && head_dim != 128) return fail(E_UNSUPPORTED, "cells_attn: head_dim %lld (128 or 256)",
+                                                      (long long)head_dim);
+  if (n_cells <= 0 || kv_len <= 0) return fail(E_SHAPE, "cells_attn: %lld cells of %lld", (long long)n_cells,
+                                                (long long)kv_len);
+  if (hkv * kv_len * head_dim * 2 > (int64_t)UINT32_MAX)
+    return fail(E_UNSUPPORTED, "cells_attn: a K or V cache of more than 4 GiB");
+  if (!q || !k || !v || !cells || !real || !out) return fail(E_ARG, "cells_attn: null pointer");
+  if (((uintptr_t)q | (uintptr_t)k | (uintptr_t)v) & 15)
+    return fail(E_ARG, "cells_attn: q, k and v must be 16-byte aligned");
+  const size_t need = sh_cells_attn_workspace(n_q, hq, hkv, head_dim, n_cells);
+  if (!workspace || workspace_bytes < need)
+    return fail(E_WORKSPACE, "cells_attn: workspace of %zu bytes, %zu needed", workspace_bytes, need);
+  AttnArgs a{};
+  a.q = q;
+  a.k = k;
+  a.v = v;
+  a.table = cells;
+  a.real = real;
+  a.ws = (float*)workspace;
+  a.out = out;
+  a.n_q = (int)n_q;
+  a.hq = (int)hq;
+  a.hkv = (int)hkv;
+  a.ctx = (int)n_cells;
+  a.kv_len = kv_len;
+  a.tiles = (int)((n_cells + 15) / 16);
+  a.units = (int)(n_q * hkv);
+  a.rows = (int)(hq / hkv);
+  a.scale_log2 = scale * 1.4426950408889634f;
+  return with_half_dtype(dtype, [&](auto* tp) {
+    using XT = std::remove_pointer_t<decltype(tp)>;
+    return head_dim == 256 ? launch_attn<XT, 256, true>(a, (hipStream_t)stream)
+                           : launch_attn<XT, 128, true>(a, (hipStream_t)stream);
+  });
+}
+
+}  // extern "C"

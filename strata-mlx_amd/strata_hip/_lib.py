@@ -45,10 +45,17 @@ PROTOTYPES = {
     "sh_stack_matvec": [c_int, c_vp, c_vp, c_i64, c_i64, c_i64, c_vp, c_int, c_i64, c_vp, c_vp, c_sz, c_vp],
     "sh_moe_decode_phase": [c_int, c_int, c_int, c_vp, c_vp, c_vp, c_i64, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_int,
                             c_vp, c_int, c_i64, c_i64, c_i64, c_i64, c_vp, c_vp, c_sz, c_vp],
+    "sh_paged_attn_workspace": [c_i64, c_i64, c_i64, c_i64, c_i64],
+    "sh_paged_attn": [c_vp, c_vp, c_vp, c_vp, c_i64, c_i64, c_i64, c_i64, c_i64, c_i64, ctypes.c_float, c_int, c_vp,
+                      c_vp, c_sz, c_vp],
+    "sh_cells_attn_workspace": [c_i64, c_i64, c_i64, c_i64, c_i64],
+    "sh_cells_attn": [c_vp, c_vp, c_vp, c_i64, c_vp, c_vp, c_i64, c_i64, c_i64, c_i64, c_i64, ctypes.c_float, c_int,
+                      c_vp, c_vp, c_sz, c_vp],
 }
 _RESTYPE = {"sh_last_error": ctypes.c_char_p, "sh_tables_bytes": c_sz, "sh_tiles_workspace": c_sz,
             "sh_tiles_most": c_i64, "sh_switch_workspace": c_sz,
-            "sh_moe_workspace": c_sz, "sh_stack_workspace": c_sz}
+            "sh_moe_workspace": c_sz, "sh_stack_workspace": c_sz, "sh_paged_attn_workspace": c_sz,
+            "sh_cells_attn_workspace": c_sz}
 
 _lib = None
 
