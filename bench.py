@@ -117,6 +117,57 @@ def matvec_stream(dev, steps, warmup):
     return res
 
 
+def attention_decode(dev, steps, warmup):
+    """C4: paged GQA decode attention, 16 query heads over 2 KV heads of 256, pages of 16, contexts 4K / 32K / 128K,
+    B = 1, 2, 4, 8 queries causal among themselves. Each context's layers are distinct KV pools (shuffled page
+    tables) totalling >= 512 MB, so the Infinity Cache holds none of them; a captured graph runs every layer once.
+    Bytes a call: K and V of the context (2,048 B a position) + page table + q and out."""
+    import torch
+
+    from strata_hip import attention as SA
+
+    Hq, Hkv, Dh = 16, 2, 256
+    res = {}
+    for ctx in (4096, 32768, 131072):
+        n_pages = ctx // 16
+        pool = ctx * 2 * Hkv * Dh * 2
+        n_layers = max(2, -(-512 * 2**20 // pool))
+        gen = torch.Generator(device=dev)
+        gen.manual_seed(ctx)
+        ks = [torch.randn(n_pages, Hkv, 16, Dh, device=dev, generator=gen).to(torch.bfloat16) for _ in range(n_layers)]
+        vs = [torch.randn(n_pages, Hkv, 16, Dh, device=dev, generator=gen).to(torch.bfloat16) for _ in range(n_layers)]
+        tabs = [torch.randperm(n_pages, device=dev, generator=gen).to(torch.int32) for _ in range(n_layers)]
+        res[str(ctx)] = {}
+        for b in (1, 2, 4, 8):
+            qs = [torch.randn(b, Hq, Dh, device=dev, generator=gen).to(torch.bfloat16) for _ in range(n_layers)]
+            stream = torch.cuda.Stream()
+            with torch.cuda.stream(stream):
+                for i in range(n_layers):
+                    SA.paged_decode_attention(qs[i], ks[i], vs[i], tabs[i], ctx)
+                torch.cuda.synchronize()
+                graph = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(graph, stream=stream):
+                    for i in range(n_layers):
+                        SA.paged_decode_attention(qs[i], ks[i], vs[i], tabs[i], ctx)
+                for _ in range(warmup):
+                    graph.replay()
+                torch.cuda.synchronize()
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                e0.record(stream)
+                for _ in range(steps):
+                    graph.replay()
+                e1.record(stream)
+                torch.cuda.synchronize()
+            sec = e0.elapsed_time(e1) * 1e-3 / (steps * n_layers)
+            nbytes = ctx * 2 * Hkv * Dh * 2 + n_pages * 4 + 2 * b * Hq * Dh * 2
+            res[str(ctx)][str(b)] = {"us": round(sec * 1e6, 2), "GBps": round(nbytes / sec / 1e9, 1),
+                                     "frac": round(nbytes / sec / 1e9 / HBM_PEAK_GBS, 4), "layers": n_layers}
+            print(f"# C4 ctx={ctx} B={b}: {res[str(ctx)][str(b)]}", file=sys.stderr, flush=True)
+        del ks, vs, tabs
+        torch.cuda.empty_cache()
+    return res
+
+
 def cpu_baseline(raw, inputs, kind, seconds, check_outputs):
     """The oracle's restatement of the reference's CPU path (dequantize the touched experts, numpy matmul in
     float32, the reference's routing, SwiGLU and combine roundings), one thread, on the host cores."""
@@ -184,6 +235,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-matvec", action="store_true")
+    ap.add_argument("--no-attention", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: --gpus {args.gpus}: this path is measured on one GPU (expert parallelism across GPUs is "
@@ -268,6 +320,7 @@ def main():
         print(f"# B={b}: {per_batch[b]}", file=sys.stderr, flush=True)
 
     matvec = None if args.no_matvec else matvec_stream(dev, max(3, args.steps // 4), args.warmup)
+    attention = None if args.no_attention else attention_decode(dev, max(3, args.steps // 4), args.warmup)
     value = all_bytes / all_time / 1e9
     achieved = gu_bytes / gu_time / 1e9
     traffic = None
@@ -287,6 +340,7 @@ def main():
                    "step": "one decode pass through the layers at each batch width"},
         "per_batch": {str(k): v for k, v in per_batch.items()},
         "matvec_3072x2048": matvec,
+        "paged_attention": attention,
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic, "kernel": "k_moe_gate_up",
                      "bytes_per_launch": round(gu_bytes / gu_launches), "launches": gu_launches,

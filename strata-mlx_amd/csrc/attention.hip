@@ -13,8 +13,9 @@
 //        lane (g, n) holds the scores of positions 4g..4g+3 for query row n;
 //   O += P V:    that is exactly the A operand layout of P for 16x16x16 (row n, positions 4g..4g+3); V (16 x D)
 //        is the B operand, read from LDS; O[row 4g + i][dim n] accumulates in registers, 16 dims a tile.
-// The block's tiles come into LDS by direct 16-byte loads (no registers), two steps of tiles in flight; rows of K
-// and V sit at a 528-byte stride (33 chunks), so the 16 positions a read touches fall in distinct banks.
+// The block's tiles come into LDS by direct 16-byte loads (no registers), two steps of tiles in flight, every
+// destination below 128 KiB. Rows of K and V are not padded: chunk c of position r sits at chunk c ^ (r % 16) of
+// its row, so the 16 positions a K read touches, and the 4 rows a V read touches, fall in distinct banks.
 #include <type_traits>
 
 #include "launch.h"
@@ -37,9 +38,9 @@ struct AttnArgs {
 };
 
 constexpr int ATT_WAVES = 4, ATT_NT = 256;
-template <int D> constexpr int att_part_slots() { return 16 * (D / 8 + 1); }  // a tile's K or V, padded rows
-template <int D> constexpr int att_part_insts() { return (att_part_slots<D>() + 63) / 64; }
-template <int D> constexpr int att_part_bytes() { return att_part_insts<D>() * 64 * 16; }
+constexpr int ATT_DMA_LIMIT = 128 * 1024;             // direct loads into LDS land below this address
+template <int D> constexpr int att_part_insts() { return 16 * D / 8 / 64; }  // a tile's K or V: 16 rows of D
+template <int D> constexpr int att_part_bytes() { return 16 * D * 2; }
 
 template <typename XT> __device__ __forceinline__ f32x4 mfma16x16x16(uint32_t a0, uint32_t a1, uint32_t b0, uint32_t b1,
                                                                      f32x4 c) {
@@ -61,8 +62,8 @@ template <typename XT> __device__ __forceinline__ uint32_t pack_pair(float lo, f
 // (rt, ph) multiplies row tile rt against the step's tile ph.
 template <typename XT, int D, bool CELLS>
 __global__ __launch_bounds__(ATT_NT) void k_attn_split(AttnArgs a) {
-  constexpr int NC = D / 32, NDT = D / 16, PS = att_part_slots<D>(), PI = att_part_insts<D>();
-  constexpr int PB = att_part_bytes<D>(), RS = (D / 8 + 1) * 16;  // bytes a staged row
+  constexpr int NC = D / 32, NDT = D / 16, PI = att_part_insts<D>(), NCH = D / 8;  // NCH: chunks a row
+  constexpr int PB = att_part_bytes<D>(), RS = D * 2;  // bytes a staged row
   extern __shared__ u32x4 dyn[];
   const uint32_t lds_base = SH_LDS_ADDR(dyn);
   const uint8_t* lds = (const uint8_t*)dyn;
@@ -84,13 +85,26 @@ __global__ __launch_bounds__(ATT_NT) void k_attn_split(AttnArgs a) {
   const int my_insts = (n_inst - wave + ATT_WAVES - 1) / ATT_WAVES;
   const XT* kb = (const XT*)a.k;
   const XT* vb = (const XT*)a.v;
+  // the split's page ids (paged) or cell ids and flags (cells), staged in LDS once: the loads of a step then
+  // wait on no global read
+  int32_t* tab = (int32_t*)(lds + 2 * step_bytes);
+  uint8_t* flags = (uint8_t*)(tab + (CELLS ? 16 : 1) * a.tiles_per_split);
+  {
+    const int n = CELLS ? min(16 * (t1 - t0), a.ctx - 16 * t0) : t1 - t0;
+    const int32_t* src = CELLS ? a.table + (int64_t)qcell * a.ctx + 16 * t0 : a.table + t0;
+    for (int i = threadIdx.x; i < n; i += ATT_NT) tab[i] = src[i];
+    if constexpr (CELLS) {
+      const uint8_t* rs = a.real + (int64_t)qcell * a.ctx + 16 * t0;
+      for (int i = threadIdx.x; i < 16 * (t1 - t0); i += ATT_NT) flags[i] = i < n ? rs[i] : 0;
+    }
+    lds_sync();
+  }
   auto row_off = [&](int tile, int tok) -> int64_t {  // elements from the K / V base to a tile position's row
     if constexpr (CELLS) {
-      const int pos = min(tile * 16 + tok, a.ctx - 1);
-      const int cell = a.table[(int64_t)qcell * a.ctx + pos];
-      return ((int64_t)h * a.kv_len + cell) * D;
+      const int i = min((tile - t0) * 16 + tok, a.ctx - 16 * t0 - 1);
+      return ((int64_t)h * a.kv_len + tab[i]) * D;
     } else {
-      const int64_t phys = a.table[min(tile, a.tiles - 1)];
+      const int64_t phys = tab[tile - t0];
       return ((phys * a.hkv + h) * 16 + tok) * D;
     }
   };
@@ -99,9 +113,8 @@ __global__ __launch_bounds__(ATT_NT) void k_attn_split(AttnArgs a) {
     for (int q = wave; q < n_inst; q += ATT_WAVES) {
       const int part = q / PI, j = q - part * PI;  // part: tile ph' = part / 2, K (0) or V (1)
       const int tile = min(t0 + step * PL + part / 2, t1 - 1);
-      const int s = j * 64 + lane;
-      const int tok = min(s / (D / 8 + 1), 15);
-      const int piece = min(s - (s / (D / 8 + 1)) * (D / 8 + 1), D / 8 - 1);
+      const int s = j * 64 + lane;                          // slot: chunk s % NCH of row s / NCH
+      const int tok = s / NCH, piece = (s % NCH) ^ (tok & 15);  // the chunk that slot holds
       const int64_t off = (row_off(tile, tok) + 8 * piece) * (int64_t)sizeof(XT);
       lds_dma16(part & 1 ? (const void*)vb : (const void*)kb, (uint32_t)off, buf + part * PB + j * 1024);
     }
@@ -137,7 +150,7 @@ __global__ __launch_bounds__(ATT_NT) void k_attn_split(AttnArgs a) {
       f32x4 S = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
       for (int c = 0; c < NC; ++c) {
-        const u32x4 kf = *(const u32x4*)(kt + n * RS + c * 64 + 16 * g);
+        const u32x4 kf = *(const u32x4*)(kt + n * RS + 16 * ((4 * c + g) ^ n));
         S = mfma<XT>(kf, qf[c], S);
       }
       float sv[4], mx = -INFINITY;
@@ -145,7 +158,7 @@ __global__ __launch_bounds__(ATT_NT) void k_attn_split(AttnArgs a) {
       for (int i = 0; i < 4; ++i) {
         const int pos = tile * 16 + 4 * g + i;
         bool ok;
-        if constexpr (CELLS) ok = pos < a.ctx && a.real[(int64_t)qcell * a.ctx + pos] != 0;
+        if constexpr (CELLS) ok = flags[pos - 16 * t0] != 0;
         else ok = pos < a.ctx && pos <= vis_last;
         sv[i] = ok ? S[i] * a.scale_log2 : -INFINITY;
         mx = fmaxf(mx, sv[i]);
@@ -178,9 +191,9 @@ __global__ __launch_bounds__(ATT_NT) void k_attn_split(AttnArgs a) {
       const uint32_t pa0 = pack_pair<XT>(p[0], p[1]), pa1 = pack_pair<XT>(p[2], p[3]);
 #pragma unroll
       for (int dt = 0; dt < NDT; ++dt) {
-        const uint8_t* vc = vt + (16 * dt + n) * 2;
-        const uint32_t v0 = *(const uint16_t*)(vc + (4 * g + 0) * RS), v1 = *(const uint16_t*)(vc + (4 * g + 1) * RS);
-        const uint32_t v2 = *(const uint16_t*)(vc + (4 * g + 2) * RS), v3 = *(const uint16_t*)(vc + (4 * g + 3) * RS);
+        const int cv = 2 * dt + (n >> 3), e2 = (n & 7) * 2;  // the chunk and byte of dim 16 dt + n
+        auto vat = [&](int r) { return (uint32_t) * (const uint16_t*)(vt + r * RS + 16 * (cv ^ (r & 15)) + e2); };
+        const uint32_t v0 = vat(4 * g), v1 = vat(4 * g + 1), v2 = vat(4 * g + 2), v3 = vat(4 * g + 3);
         O[dt] = mfma16x16x16<XT>(pa0, pa1, v0 | (v1 << 16), v2 | (v3 << 16), O[dt]);
       }
     }
@@ -241,9 +254,28 @@ __global__ __launch_bounds__(ATT_NT) void k_attn_split(AttnArgs a) {
 }
 
 // merge the splits of one (unit, row): out = sum_s O_s 2^(m_s - m) / sum_s l_s 2^(m_s - m); a row that sees no
-// position (every cell masked) gives zeros
+// position (every cell masked) gives zeros. The splits' factors are worked out once into LDS by the block's
+// threads together; then thread d sums dimension d over the splits.
+constexpr int ATT_MAX_SPLITS = 1024;
+
+__device__ __forceinline__ float block_reduce(float v, bool is_max, float* scratch) {
+  for (int o = 32; o > 0; o >>= 1) {
+    const float w = __shfl_xor(v, o);
+    v = is_max ? fmaxf(v, w) : v + w;
+  }
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+  __syncthreads();
+  if (lane == 0) scratch[wave] = v;
+  __syncthreads();
+  v = scratch[0];
+  for (int i = 1; i < nw; ++i) v = is_max ? fmaxf(v, scratch[i]) : v + scratch[i];
+  return v;
+}
+
 template <typename XT, int D, bool CELLS>
 __global__ __launch_bounds__(256) void k_attn_merge(AttnArgs a) {
+  __shared__ float fac[ATT_MAX_SPLITS];
+  __shared__ float scratch[8];
   const int unit = blockIdx.y, row = blockIdx.x;
   const int group = a.hq / a.hkv;
   const int h = CELLS ? unit % a.hkv : unit;
@@ -251,15 +283,22 @@ __global__ __launch_bounds__(256) void k_attn_merge(AttnArgs a) {
   const int64_t stride = (int64_t)a.units * a.rows * (D + 2);
   const float* w0 = a.ws + ((int64_t)unit * a.rows + row) * (D + 2);
   float m = -INFINITY;
-  for (int s = 0; s < a.splits; ++s) m = fmaxf(m, w0[s * stride]);
+  for (int s = threadIdx.x; s < a.splits; s += blockDim.x) m = fmaxf(m, w0[s * stride]);
+  m = block_reduce(m, true, scratch);
   const float base = m == -INFINITY ? 0.0f : m;
   float l = 0.0f;
-  for (int s = 0; s < a.splits; ++s) l += w0[s * stride + 1] * exp2f(w0[s * stride] - base);
+  for (int s = threadIdx.x; s < a.splits; s += blockDim.x) {
+    const float f = exp2f(w0[s * stride] - base);
+    fac[s] = f;
+    l += w0[s * stride + 1] * f;
+  }
+  l = block_reduce(l, false, scratch);  // its barriers also publish fac
   const float inv = l > 0.0f ? 1.0f / l : 0.0f;
   XT* o = (XT*)a.out + ((int64_t)qt * a.hq + qh) * D;
   for (int d = threadIdx.x; d < D; d += blockDim.x) {
     float acc = 0.0f;
-    for (int s = 0; s < a.splits; ++s) acc += w0[s * stride + 2 + d] * exp2f(w0[s * stride] - base);
+#pragma unroll 8
+    for (int s = 0; s < a.splits; ++s) acc += w0[s * stride + 2 + d] * fac[s];
     o[d] = from_f32<XT>(acc * inv);
   }
 }
@@ -275,25 +314,37 @@ static int attn_cus() {
   return cus;
 }
 
-// splits of the context: enough blocks to fill the chip twice over, at least 4 tiles a split
-static void plan_splits(AttnArgs& a, int zgroups) {
-  const int64_t want = 2 * (int64_t)attn_cus();
+// splits of the context: enough blocks to fill the chip four times over, at least one step of tiles a split
+// (`min_tiles`), at most ATT_MAX_SPLITS splits
+static void plan_splits(AttnArgs& a, int zgroups, int min_tiles) {
+  const int64_t want = 4 * (int64_t)attn_cus();
   const int64_t per_unit = std::max<int64_t>(1, want / ((int64_t)a.units * zgroups));
-  a.tiles_per_split = (int)std::max<int64_t>(4, (a.tiles + per_unit - 1) / per_unit);
-  a.splits = (a.tiles + a.tiles_per_split - 1) / a.tiles_per_split;
+  int64_t tps = std::max<int64_t>(min_tiles, (a.tiles + per_unit - 1) / per_unit);
+  tps = std::max<int64_t>(tps, (a.tiles + ATT_MAX_SPLITS - 1) / ATT_MAX_SPLITS);
+  a.tiles_per_split = (int)tps;
+  a.splits = (int)((a.tiles + tps - 1) / tps);
 }
 
-template <int D> static size_t attn_lds(int rows_here) {
-  const int RT = (rows_here + 15) / 16, RT4 = RT <= 1 ? 1 : RT <= 2 ? 2 : 4, PL = ATT_WAVES / RT4;
+static int att_phases(int rows_here) {
+  const int RT = (rows_here + 15) / 16, RT4 = RT <= 1 ? 1 : RT <= 2 ? 2 : 4;
+  return ATT_WAVES / RT4;
+}
+
+template <int D, bool CELLS> static size_t attn_lds(int rows_here, int tiles_per_split) {
+  const int PL = att_phases(rows_here);
   const size_t stage = 2 * (size_t)(2 * PL * att_part_bytes<D>());
+  const size_t tabs = CELLS ? (size_t)tiles_per_split * 16 * 5 : (size_t)tiles_per_split * 4;
   const size_t merge = sizeof(float) * (2 * ATT_WAVES * 64 + (size_t)ATT_WAVES * D * 16);
-  return std::max(stage, merge);
+  return std::max(stage + ((tabs + 15) & ~(size_t)15), merge);
 }
 
 template <typename XT, int D, bool CELLS> static int launch_attn(AttnArgs a, hipStream_t stream) {
   const int zgroups = CELLS ? 1 : (a.rows + 63) / 64;
-  plan_splits(a, zgroups);
-  const size_t lds = attn_lds<D>(std::min(64, a.rows));
+  plan_splits(a, zgroups, att_phases(std::min(64, a.rows)));
+  // the last row group may have fewer rows, more tile phases and so a larger stage
+  const size_t lds = std::max(attn_lds<D, CELLS>(std::min(64, a.rows), a.tiles_per_split),
+                              attn_lds<D, CELLS>(a.rows - 64 * (zgroups - 1), a.tiles_per_split));
+  static_assert(2 * 2 * ATT_WAVES * att_part_bytes<D>() <= ATT_DMA_LIMIT, "the stage fits under the load limit");
   if (lds > 160 * 1024) return fail(E_UNSUPPORTED, "attention: %zu bytes of LDS", lds);
   hipLaunchKernelGGL((k_attn_split<XT, D, CELLS>), dim3(a.splits, a.units, zgroups), dim3(ATT_NT), lds, stream, a);
   int st = check_launch("attention split");
@@ -306,7 +357,7 @@ static size_t attn_ws_bytes(int units, int rows, int tiles, int zgroups, int D) 
   AttnArgs a{};
   a.units = units;
   a.tiles = tiles;
-  plan_splits(a, zgroups);
+  plan_splits(a, zgroups, att_phases(std::min(64, rows)));
   return (size_t)a.splits * units * rows * (D + 2) * sizeof(float);
 }
 

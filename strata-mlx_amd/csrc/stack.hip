@@ -387,8 +387,15 @@ static int launch_stack(const uint8_t* blocks, const uint8_t* tables, int64_t n_
   P.ring_off = KIND == IQ3_S ? IQ3S_SIGNED_BYTES : 0;
   const size_t red = (size_t)(P.kw - 1) * P.rg * 64 * TPG * 4, tail = 128;
   const size_t cap = 160 * 1024;
+  // direct loads into LDS land below 128 KiB: the table and the ring stay under it
+  const size_t dma_limit = 128 * 1024;
   P.nbuf = 3;
-  while (P.nbuf > 2 && (size_t)P.ring_off + (size_t)P.nbuf * P.buf_bytes + red + tail > cap) --P.nbuf;
+  while (P.nbuf > 2 && ((size_t)P.ring_off + (size_t)P.nbuf * P.buf_bytes + red + tail > cap ||
+                        (size_t)P.ring_off + (size_t)P.nbuf * P.buf_bytes > dma_limit))
+    --P.nbuf;
+  if ((size_t)P.ring_off + (size_t)P.nbuf * P.buf_bytes > dma_limit)
+    return fail(E_UNSUPPORTED, "stack_matvec: a ring of %d x %d bytes past the 128 KiB direct-load range", P.nbuf,
+                P.buf_bytes);
   P.red_off = P.ring_off + P.nbuf * P.buf_bytes;
   const size_t lds = (size_t)P.red_off + red + tail;
   if (lds > cap) return fail(E_UNSUPPORTED, "stack_matvec: %zu bytes of LDS", lds);
