@@ -141,6 +141,7 @@ def attention_decode(dev, steps, warmup):
         for b in (1, 2, 4, 8):
             qs = [torch.randn(b, Hq, Dh, device=dev, generator=gen).to(torch.bfloat16) for _ in range(n_layers)]
             stream = torch.cuda.Stream()
+            stream.wait_stream(torch.cuda.current_stream())  # the inputs were made on the default stream
             with torch.cuda.stream(stream):
                 for i in range(n_layers):
                     SA.paged_decode_attention(qs[i], ks[i], vs[i], tabs[i], ctx)
@@ -271,6 +272,7 @@ def main():
         outs = [torch.empty(b, D, device=dev, dtype=torch.bfloat16) for _ in layers]
         uniq = [int(torch.unique(SF.top_k(lg, K)).numel()) for lg in logits]
         bytes_pass = sum(layer_bytes(u, b) for u in uniq)
+        stream.wait_stream(torch.cuda.current_stream())  # the inputs were made on the default stream
         with torch.cuda.stream(stream):
             for m, lg, x, o in zip(layers, logits, xs, outs):  # first calls allocate the workspaces
                 m(lg, x, out=o)

@@ -32,7 +32,7 @@ struct AttnArgs {
   float* ws;                 // [splits][units][rows][D + 2]: max, sum, output
   void* out;                 // (n_q, hq, D)
   int n_q, hq, hkv, ctx;     // ctx: paged context length, or cells a query
-  int64_t kv_len;            // cells: rows of one KV head
+  int64_t kv_len;            // cells: rows of one KV head; paged: pages in the pool
   int tiles, tiles_per_split, splits, units, rows;  // rows: query rows of a unit (paged n_q * group, cells group)
   float scale_log2;          // scale * log2(e)
 };
@@ -92,7 +92,9 @@ __global__ __launch_bounds__(ATT_NT) void k_attn_split(AttnArgs a) {
   {
     const int n = CELLS ? min(16 * (t1 - t0), a.ctx - 16 * t0) : t1 - t0;
     const int32_t* src = CELLS ? a.table + (int64_t)qcell * a.ctx + 16 * t0 : a.table + t0;
-    for (int i = threadIdx.x; i < n; i += ATT_NT) tab[i] = src[i];
+    // ids outside the pool are clamped into it: a bad table gives wrong numbers, never a load outside K and V
+    const int hi = (int)(a.kv_len - 1);
+    for (int i = threadIdx.x; i < n; i += ATT_NT) tab[i] = min(max(src[i], 0), hi);
     if constexpr (CELLS) {
       const uint8_t* rs = a.real + (int64_t)qcell * a.ctx + 16 * t0;
       for (int i = threadIdx.x; i < 16 * (t1 - t0); i += ATT_NT) flags[i] = i < n ? rs[i] : 0;
@@ -399,6 +401,7 @@ int sh_paged_attn(const void* q, const void* k_pages, const void* v_pages, const
   a.v = v_pages;
   a.table = page_table;
   a.real = nullptr;
+  a.kv_len = n_pages;
   a.ws = (float*)workspace;
   a.out = out;
   a.n_q = (int)n_q;
