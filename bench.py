@@ -169,6 +169,61 @@ def attention_decode(dev, steps, warmup):
     return res
 
 
+def prefill_layer(dev, steps, warmup):
+    """C5: a 2048-token prompt chunk through one MoE layer's routed experts: top-10 of 512 under Zipf(1.1)
+    popularity, IQ3_S experts (gate / up 512 x 2048, down 2048 x 512), pairs in tiles of 16 by tiles_of, the three
+    grouped GEMMs on MFMA with the weights dequantized into LDS as bf16. Timed: tiles_of + the three products +
+    the SwiGLU between them, as one captured graph. MFMA use = 2 * pairs * (3 * 512 * 2048) flops / time against
+    the 2.5 PFLOP/s dense bf16 peak."""
+    import numpy as np
+    import torch
+
+    from strata_hip import blocks as SB
+    from strata_hip import synth
+
+    T_, E_, K_, D_, F_ = 2048, 512, 10, 2048, 512
+    rng = np.random.default_rng(5)
+    logits = synth.zipf_logits(rng, T_, E_).to(dev)
+    x = torch.from_numpy(rng.standard_normal((T_, D_)).astype(np.float32)).to(torch.bfloat16).to(dev)
+    gate = SB.BlockSwitchLinear(synth.random_blocks_gpu("IQ3_S", E_ * F_, D_, 11, dev), "IQ3_S", (E_, F_, D_))
+    up = SB.BlockSwitchLinear(synth.random_blocks_gpu("IQ3_S", E_ * F_, D_, 12, dev), "IQ3_S", (E_, F_, D_))
+    down = SB.BlockSwitchLinear(synth.random_blocks_gpu("IQ3_S", E_ * D_, F_, 13, dev), "IQ3_S", (E_, D_, F_))
+    from strata_hip import fused as SF
+    idx = SF.top_k(logits, K_)
+    pairs = idx.numel()
+    torch.cuda.synchronize()
+
+    def layer():
+        return SB._tiled_glu(x[None], idx[None], up, gate, down)
+
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        layer()
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream):
+            layer()
+        for _ in range(warmup):
+            graph.replay()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(steps):
+            graph.replay()
+        e1.record(stream)
+        torch.cuda.synchronize()
+    sec = e0.elapsed_time(e1) * 1e-3 / steps
+    flops = 2 * pairs * 3 * F_ * D_
+    counts = torch.bincount(idx.reshape(-1).long(), minlength=E_)
+    tiles = int(((counts + 15) // 16).sum())
+    res = {"us": round(sec * 1e6, 1), "TFLOPs": round(flops / sec / 1e12, 1),
+           "mfma_frac": round(flops / sec / 2.5e15, 4), "pairs": pairs, "tiles": tiles,
+           "top_expert_pairs": int(counts.max()), "experts_used": int((counts > 0).sum())}
+    print(f"# C5 prefill: {res}", file=sys.stderr, flush=True)
+    return res
+
+
 def cpu_baseline(raw, inputs, kind, seconds, check_outputs):
     """The oracle's restatement of the reference's CPU path (dequantize the touched experts, numpy matmul in
     float32, the reference's routing, SwiGLU and combine roundings), one thread, on the host cores."""
@@ -237,6 +292,7 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-matvec", action="store_true")
     ap.add_argument("--no-attention", action="store_true")
+    ap.add_argument("--no-prefill", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: --gpus {args.gpus}: this path is measured on one GPU (expert parallelism across GPUs is "
@@ -323,6 +379,7 @@ def main():
 
     matvec = None if args.no_matvec else matvec_stream(dev, max(3, args.steps // 4), args.warmup)
     attention = None if args.no_attention else attention_decode(dev, max(3, args.steps // 4), args.warmup)
+    prefill = None if args.no_prefill else prefill_layer(dev, max(3, args.steps // 4), args.warmup)
     value = all_bytes / all_time / 1e9
     achieved = gu_bytes / gu_time / 1e9
     traffic = None
@@ -343,6 +400,7 @@ def main():
         "per_batch": {str(k): v for k, v in per_batch.items()},
         "matvec_3072x2048": matvec,
         "paged_attention": attention,
+        "prefill_layer": prefill,
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic, "kernel": "k_moe_gate_up",
                      "bytes_per_launch": round(gu_bytes / gu_launches), "launches": gu_launches,

@@ -150,6 +150,13 @@ int sh_moe_decode_phase(int phase, int kind, int kind_down, const void* gate, co
                         const void* x, int dtype, int64_t tokens, int64_t k, int64_t d_model, int64_t d_ff, void* out,
                         void* workspace, size_t workspace_bytes, void* stream);
 
+/* ---- prompts: the grouped expert GEMM over tiles of 16 pairs (strata_mlx/blocks.py:465-536, tile_matmul):
+ * out[p] = W[tile_expert[p / 16]] . a[p] for a stack of `experts` (rows, cols) layers of `kind` blocks; a (pairs,
+ * cols) bf16 or fp16 (the weights rounded to it), out (pairs, rows) fp32; rows % 64 == 0, cols % 64 == 0, pairs %
+ * 16 == 0; rows of tiles naming no expert (tile_expert outside 0..experts-1) are left as they were. */
+int sh_tile_matmul(int kind, const void* blocks, const void* tables, int64_t experts, int64_t rows, int64_t cols,
+                   const void* a, int a_dtype, int64_t pairs, const int32_t* tile_expert, float* out, void* stream);
+
 /* ---- decode attention (strata_mlx/attention.py:118-165) */
 
 /* _gathered over a page table (attention.py:144-165 with cells = page_table[p / 16] * 16 + p % 16): q (n_q, hq,
