@@ -324,8 +324,13 @@ def _lookup_glu(x, indices, up, gate, down):
 # ---- prompts: pairs in tiles of one expert, under MFMA (tiles.hip)
 
 def tileable(kind: str, rows: int, cols: int) -> bool:
-    """Whether `tile_matmul` takes a stack of such layers (strata_mlx/blocks.py:511-513)."""
-    return rows % ROWS_TILE == 0 and cols % COLS_TILE == 0 and cols % BLOCK[kind][0] == 0
+    """Whether `tile_matmul` takes a stack of such layers (strata_mlx/blocks.py:511-513): the reference's rule
+    (rows % 64, cols % 64, whole blocks), with columns in whole chunks of 256 and a row group of 64 rows that fits
+    in LDS beside the chunk buffers."""
+    rb = row_bytes(kind, cols) if cols % BLOCK[kind][0] == 0 else 0
+    room = 160 * 1024 - 2 * 64 * 256 * 2 - (32 * 1024 if kind == "IQ3_S" else 0 if kind in ("Q2_0", "Q3_K") else 16512)
+    return (rows % ROWS_TILE == 0 and cols % COLS_TILE == 0 and cols % BLOCK[kind][0] == 0 and cols % 256 == 0
+            and 64 * rb <= room)
 
 
 def tiles_of(indices: torch.Tensor, experts: int) -> tuple:
