@@ -48,11 +48,15 @@ def _signed(values: np.ndarray, sign_bits: np.ndarray) -> np.ndarray:
     return np.where(neg == 1, -values, values)
 
 
+# byte value -> its four codes less one, weight 4i + j from bits 2j..2j+1 of byte i
+_Q2_CODES = (((np.arange(256, dtype=np.uint32)[:, None] >> (2 * np.arange(4, dtype=np.uint32))) & 3).astype(f32)
+             - f32(1))
+
+
 def _q2_0(b, t):  # blocks.py:58-68
     d = _f16(b, 0)
-    q = b[:, 2:18].astype(np.uint32)  # 16 bytes, byte i holds weights 4i..4i+3
-    codes = np.stack([(q >> (2 * j)) & 3 for j in range(4)], axis=2).reshape(len(b), 64)
-    return d[:, None] * (codes.astype(f32) - f32(1))
+    codes = _Q2_CODES[b[:, 2:18]].reshape(len(b), 64)  # 16 bytes, byte i holds weights 4i..4i+3
+    return d[:, None] * codes
 
 
 def _iq4_nl(b, t):  # blocks.py:69-77

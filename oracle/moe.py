@@ -41,3 +41,28 @@ def moe_decode(logits, x, k, stacks, shared, shared_gate, dtype="bfloat16"):
     s = expert_products(*shared, zero, x, dtype)[:, 0, :]
     g = R.round_to(np.asarray(x, np.float64) @ np.asarray(shared_gate, np.float64), dtype)
     return R.moe_combine(y, w, g, s, dtype), idx, w
+
+
+def moe_decode_blocks(logits, x, k, fetch, kinds, dims, shared, shared_gate, tables, dtype="bfloat16"):
+    """moe_decode over experts kept as GGUF blocks, dequantizing only the experts the window chooses (a layer of
+    512 experts would be 6 GB of float32). fetch = (gate, up, down): callables giving expert e's uint8 blocks;
+    kinds = (kind of gate / up, kind of down); dims = (E, d, f); shared = (gate, up, down) float32 (1, ...).
+    Returns (out, idx, w)."""
+    E, d, f = dims
+    logits32 = np.asarray(logits, np.float32)
+    idx = R.top_k(logits32, k)
+    used = np.unique(idx)
+    pos = np.zeros(E, dtype=np.int64)
+    pos[used] = np.arange(used.size)
+
+    def take(get, kind, rows, cols):
+        part = np.concatenate([np.asarray(get(int(e)), np.uint8).reshape(-1) for e in used])
+        return B.dequantize(part, kind, (used.size, rows, cols), tables)
+
+    stacks = (take(fetch[0], kinds[0], f, d), take(fetch[1], kinds[0], f, d), take(fetch[2], kinds[1], d, f))
+    w = R.routing_weights(logits32, idx)
+    y = expert_products(*stacks, pos[idx], x, dtype)
+    zero = np.zeros((x.shape[0], 1), dtype=np.int64)
+    s = expert_products(*shared, zero, x, dtype)[:, 0, :]
+    g = R.round_to(np.asarray(x, np.float64) @ np.asarray(shared_gate, np.float64), dtype)
+    return R.moe_combine(y, w, g, s, dtype), idx, w

@@ -68,4 +68,13 @@ inline int lanes_per_row(int64_t runs) {
   return p;
 }
 
+// LDS a workgroup may hold on gfx950, and the static LDS a kernel declares: a launch asking for more than the
+// sum fits is refused by the queue (an invalid allocation that ends the process), so launches check it first
+constexpr size_t LDS_BYTES = 160 * 1024;
+template <typename K> inline size_t static_lds(K* kern) {
+  hipFuncAttributes attr;
+  if (hipFuncGetAttributes(&attr, (const void*)kern) != hipSuccess) return LDS_BYTES;
+  return attr.sharedSizeBytes;
+}
+
 }  // namespace sh

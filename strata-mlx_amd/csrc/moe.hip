@@ -17,6 +17,7 @@
 // order its MFMA fragments take them, and are read straight from memory (L2). Grids are sized by the most groups
 // there could be (B*k + 1); blocks past the groups the route found leave at once, so nothing waits on the host.
 #include "launch.h"
+#include "regmac.h"
 #include "xmv.h"
 
 namespace sh {
@@ -290,9 +291,217 @@ __global__ __launch_bounds__(256) void k_moe_gate_up(const uint8_t* __restrict__
   }
 }
 
+// ---- route, gate and up in one kernel, for the common shape (512 experts, d_model 2048)
+//
+// Every block routes the whole window again (B tokens' top-k of 512 logits: a few microseconds of arithmetic on
+// data in L2), so no kernel boundary stands between the choice and the expert products. The groups are the chosen
+// experts in ascending order, then the shared expert; block (x, g) takes 16 rows of gate and up of group g. Its
+// weights are staged in LDS and its tokens' activation fragments loaded into registers straight from x in the same
+// memory trip; block (0, 0) also writes the group table, the choice and its weights for the down kernel, block
+// (1, 0) the shared expert's gate logits.
+
+constexpr int FRONT_E = 512, FRONT_D = 2048;
+
+template <int KIND, int KIND_DOWN, typename XT, typename LT, int TPG>
+__global__ __launch_bounds__(256) void k_moe_front(const uint8_t* __restrict__ gate, const uint8_t* __restrict__ up,
+                                                   const uint8_t* __restrict__ sh_gate, const uint8_t* __restrict__ sh_up,
+                                                   const LT* __restrict__ logits, const XT* __restrict__ x,
+                                                   const XT* __restrict__ wgt, int K, int B, int F,
+                                                   const uint8_t* __restrict__ signed_tab, MoeWs ws) {
+  using MT = XT;
+  using RK = RouteKey<LT>;
+  using key_t = typename RK::type;
+  constexpr int E = FRONT_E, D = FRONT_D, VPL = E / 64, WORDS = E / 32;
+  constexpr int GPER = KIND == Q2_0 ? D / 64 / 4 : D / 32 / 4;  // a wave's quarter of the scale groups
+  constexpr int RB = (int)row_bytes_dev(KIND, D);
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int row0 = blockIdx.x * 16, gy = blockIdx.y;
+  const int P = B * K;
+  __shared__ int s_idx[MOE_MAX_PAIRS];
+  __shared__ float s_wt[MOE_MAX_PAIRS];
+  __shared__ uint32_t s_flag[WORDS];
+  __shared__ int s_cnt[MOE_MAX_PAIRS + 1];
+  __shared__ int s_e, s_groups, s_n, s_pair[16];
+  __shared__ float s_red[2][4][64][TPG];
+  extern __shared__ u32x4 dyn[];
+  uint8_t* tab = (uint8_t*)dyn;
+  uint8_t* wgl = tab + moe_tab_bytes<KIND>();
+  uint8_t* wul = wgl + 16 * RB + 16;
+
+  if (tid < WORDS) s_flag[tid] = 0u;
+  if (tid <= MOE_MAX_PAIRS) s_cnt[tid] = 0;
+  // 1. each token's top-k of the logits and the softmax of the chosen (a wave a token)
+  for (int t = wave; t < B; t += 4) {
+    key_t key[VPL];
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) key[i] = RK::make(logits[(int64_t)t * E + i * 64 + lane], i * 64 + lane);
+    float top = 0.0f, sum = 0.0f, my_e = 0.0f;
+    for (int r = 0; r < K; ++r) {
+      key_t best = key[0];
+#pragma unroll
+      for (int i = 1; i < VPL; ++i) best = key[i] > best ? key[i] : best;
+      best = RK::wave_max(best);
+      const float v = RK::value(best);
+      if (r == 0) top = v;
+      const float ev = expf(v - top);
+      sum += ev;
+      if (lane == r) {
+        my_e = ev;
+        s_idx[t * K + r] = RK::index(best);
+      }
+#pragma unroll
+      for (int i = 0; i < VPL; ++i)
+        if (key[i] == best) key[i] = 0;
+    }
+    if (lane < K) s_wt[t * K + lane] = my_e / sum;
+  }
+  __syncthreads();
+  if (tid < P) atomicOr(&s_flag[s_idx[tid] >> 5], 1u << (s_idx[tid] & 31));
+  __syncthreads();
+  // 2. this block's group: the gy-th chosen expert in ascending order, or the shared expert after them
+  if (wave == 0) {
+    const uint32_t word = lane < WORDS ? s_flag[lane] : 0u;
+    const int cnt = __popc(word);
+    int incl = cnt;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const int v = __shfl_up(incl, o);
+      if (lane >= o) incl += v;
+    }
+    const int total = __shfl(incl, 63), excl = incl - cnt;
+    if (lane == 0) s_groups = total + 1;
+    if (gy >= excl && gy < incl) {
+      uint32_t w = word;
+      for (int i = 0; i < gy - excl; ++i) w &= w - 1u;
+      s_e = lane * 32 + __ffs(w) - 1;
+    }
+    if (lane == 0 && gy == total) s_e = E;
+  }
+  __syncthreads();
+  const int groups = s_groups;
+
+  // block (0, 0): the group table, the choice and its weights, for the down kernel and the caller
+  if (blockIdx.x == 0 && gy == 0) {
+    int g_p = 0, rank = 0, e_p = 0;
+    if (tid < P) {
+      e_p = s_idx[tid];
+      const int w = e_p >> 5;
+      for (int i = 0; i < w; ++i) g_p += __popc(s_flag[i]);
+      g_p += __popc(s_flag[w] & ((1u << (e_p & 31)) - 1u));
+      rank = atomicAdd(&s_cnt[g_p], 1);  // order within a group: any (each token's rows are its own)
+      ws.g_pair[g_p * 16 + rank] = tid;
+      ws.idx[tid] = e_p;
+      ws.w[tid] = s_wt[tid];
+    }
+    __syncthreads();
+    if (tid < P && rank == 0) {
+      ws.g_expert[g_p] = e_p;
+      ws.g_ntok[g_p] = s_cnt[g_p];
+    }
+    if (tid == 0) {
+      ws.g_expert[groups - 1] = E;
+      ws.g_ntok[groups - 1] = B;
+      *ws.n_groups = groups;
+    }
+    if (tid < B) ws.g_pair[(groups - 1) * 16 + tid] = P + tid;
+  }
+  // block (1, 0): the shared expert's gate logit of each token, rounded to the activation type
+  if (blockIdx.x == 1 && gy == 0) {
+    for (int t = wave; t < B; t += 4) {
+      float acc = 0.0f;
+#pragma unroll
+      for (int j = 0; j < D / 512; ++j) {
+        const u32x4 xv = *(const u32x4*)(x + (int64_t)t * D + 8 * (lane + 64 * j));
+        const u32x4 wv = *(const u32x4*)(wgt + 8 * (lane + 64 * j));
+        const XT* a = (const XT*)&xv;
+        const XT* b = (const XT*)&wv;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) acc = fmaf(to_f32(a[i]), to_f32(b[i]), acc);
+      }
+      acc = wave_sum(acc);
+      if (lane == 0) ws.gsh[t] = to_f32(from_f32<XT>(acc));
+    }
+  }
+  if (gy >= groups) return;  // block-uniform: no more barriers for these blocks
+  const int e = s_e;
+  // 3. the group's pairs in token order (a token chooses an expert at most once)
+  if (wave == 0) {
+    int j_hit = -1;
+    if (e < E && lane < B)
+      for (int j = 0; j < K; ++j)
+        if (s_idx[lane * K + j] == e) j_hit = j;
+    const uint64_t bal = __ballot(j_hit >= 0);
+    if (e < E) {
+      if (j_hit >= 0) s_pair[__popcll(bal & ((1ull << lane) - 1ull))] = lane * K + j_hit;
+      if (lane == 0) s_n = __popcll(bal);
+    } else {
+      if (lane < B) s_pair[lane] = P + lane;
+      if (lane == 0) s_n = B;
+    }
+  }
+  __syncthreads();
+  const int n_tok = s_n;
+  // 4. weights to LDS and activation fragments to registers, in one memory trip
+  const int64_t ebytes = (int64_t)F * RB;
+  const uint8_t* g_src = (e == E ? sh_gate : gate + (int64_t)e * ebytes) + (int64_t)row0 * RB;
+  const uint8_t* u_src = (e == E ? sh_up : up + (int64_t)e * ebytes) + (int64_t)row0 * RB;
+  ByteStage<8> wst(wgl, g_src, 16 * RB, wul, u_src, 16 * RB);
+  wst.load(0, tid, 256);
+  int mt = lane_token<TPG>();
+  mt = mt < n_tok ? mt : 0;
+  const int pp = s_pair[mt];
+  const XT* xr = x + (int64_t)(pp < P ? pp / K : pp - P) * D;
+  XRegs<KIND, TPG, GPER> X;
+  load_x_row<KIND, XT, TPG, GPER>(X, xr, wave * GPER);
+  wst.store(0, tid, 256);
+  for (int p2 = 1; p2 < wst.passes(256); ++p2) {
+    wst.load(p2, tid, 256);
+    wst.store(p2, tid, 256);
+  }
+  if constexpr (KIND == IQ3_S) {
+    ByteStage<8> tst(tab, signed_tab, IQ3S_SIGNED_BYTES, nullptr, nullptr, 0);
+    for (int p2 = 0; p2 < tst.passes(256); ++p2) {
+      tst.load(p2, tid, 256);
+      tst.store(p2, tid, 256);
+    }
+  }
+  __syncthreads();
+  // 5. this wave's quarter of the columns of gate and of up
+  const DecodeRegs kr = decode_regs<KIND, MT>();
+  const int wcol = KIND == Q2_0 ? wave * GPER * 18 : (wave * GPER / 8) * 110;
+  float acc_g[TPG], acc_u[TPG];
+#pragma unroll
+  for (int i = 0; i < TPG; ++i) acc_g[i] = acc_u[i] = 0.0f;
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  item_mac<KIND, MT, TPG, GPER>(wgl + lead_of(g_src) + wcol, RB, X, (const uint32_t*)tab, kr, acc_g);
+  item_mac<KIND, MT, TPG, GPER>(wul + lead_of(u_src) + wcol, RB, X, (const uint32_t*)tab, kr, acc_u);
+#pragma unroll
+  for (int i = 0; i < TPG; ++i) {
+    s_red[0][wave][lane][i] = acc_g[i];
+    s_red[1][wave][lane][i] = acc_u[i];
+  }
+  __syncthreads();
+  if (wave == 0) {
+    const int g = lane >> 4, n = lane & 15;
+    float scale;
+    const int at = stage_index<KIND_DOWN, XT>(row0 + n, scale);
+#pragma unroll
+    for (int i = 0; i < TPG; ++i) {
+      const int t = g * TPG + i;
+      if (t < n_tok) {
+        const XT gv = from_f32<XT>(s_red[0][0][lane][i] + s_red[0][1][lane][i] + s_red[0][2][lane][i] + s_red[0][3][lane][i]);
+        const XT uv = from_f32<XT>(s_red[1][0][lane][i] + s_red[1][1][lane][i] + s_red[1][2][lane][i] + s_red[1][3][lane][i]);
+        ((XT*)ws.h)[(int64_t)s_pair[t] * F + at] = from_f32<XT>(to_f32(swiglu_one(gv, uv)) * scale);
+      }
+    }
+  }
+}
+
 // ---- down and the combine: a block is 16 output rows of every group's expert
 //
-// The groups go through in chunks of DOWN_CHUNK_G, their weight slices double-buffered in LDS: the next chunk's loads
+// The groups go through in chunks of cg <= DOWN_CHUNK_G (as many as LDS holds twice), their weight slices
+// double-buffered in LDS: the next chunk's loads
 // are in flight while this chunk multiplies. A wave takes every fourth group of a chunk; each pair's 16 outputs,
 // rounded to the activation type, stay in LDS for the combine at the end.
 
@@ -348,7 +557,7 @@ template <int U> struct SliceStage {
 
 template <int KIND, typename XT, int TPG>
 __global__ __launch_bounds__(256) void k_moe_down(const uint8_t* __restrict__ down, const uint8_t* __restrict__ sh_down,
-                                                  int E, int K, int B, int D, int F,
+                                                  int E, int K, int B, int D, int F, int cg,
                                                   const uint8_t* __restrict__ signed_tab, MoeWs ws, XT* __restrict__ out) {
 #pragma clang fp contract(off)
   using MT = XT;
@@ -363,7 +572,7 @@ __global__ __launch_bounds__(256) void k_moe_down(const uint8_t* __restrict__ do
   uint8_t* tab = (uint8_t*)dyn;
   const int64_t rb = row_bytes_dev(KIND, F);
   const int slot = (int)(((15 + 16 * rb + 15) >> 4) << 4);
-  uint8_t* buf[2] = {tab + moe_tab_bytes<KIND>(), tab + moe_tab_bytes<KIND>() + DOWN_CHUNK_G * slot};
+  uint8_t* buf[2] = {tab + moe_tab_bytes<KIND>(), tab + moe_tab_bytes<KIND>() + cg * slot};
 
   // the whole group table, the routing weights and the shared gate in one trip
   if (tid == 0) s_groups = *ws.n_groups;
@@ -381,17 +590,17 @@ __global__ __launch_bounds__(256) void k_moe_down(const uint8_t* __restrict__ do
   }
   __syncthreads();
   const int groups = s_groups;
-  const int chunks = (groups + DOWN_CHUNK_G - 1) / DOWN_CHUNK_G;
+  const int chunks = (groups + cg - 1) / cg;
   auto sources = [&](int c) {
-    const int g0 = c * DOWN_CHUNK_G;
-    if (tid < DOWN_CHUNK_G && g0 + tid < groups) {
+    const int g0 = c * cg;
+    if (tid < cg && g0 + tid < groups) {
       const int e = s_e[g0 + tid];
       s_src[c & 1][tid] = (e == E ? sh_down : down + (int64_t)e * D * rb) + (int64_t)row0 * rb;
     }
   };
   sources(0);
   __syncthreads();
-  SliceStage<10> st(buf[0], s_src[0], min(DOWN_CHUNK_G, groups), (int)(16 * rb), slot);
+  SliceStage<10> st(buf[0], s_src[0], min(cg, groups), (int)(16 * rb), slot);
   for (int p = 0; p < st.passes(); ++p) {
     st.load(p, tid);
     st.store(p, tid);
@@ -401,11 +610,11 @@ __global__ __launch_bounds__(256) void k_moe_down(const uint8_t* __restrict__ do
   for (int c = 0; c < chunks; ++c) {
     // the next chunk's loads go out before this chunk multiplies
     const bool more = c + 1 < chunks;
-    SliceStage<10> nx(buf[(c + 1) & 1], s_src[(c + 1) & 1], more ? min(DOWN_CHUNK_G, groups - (c + 1) * DOWN_CHUNK_G) : 0,
+    SliceStage<10> nx(buf[(c + 1) & 1], s_src[(c + 1) & 1], more ? min(cg, groups - (c + 1) * cg) : 0,
                       (int)(16 * rb), slot);
     const int single = nx.passes() == 1;
     if (more && single) nx.load(0, tid);
-    const int g0 = c * DOWN_CHUNK_G, gn = min(DOWN_CHUNK_G, groups - g0);
+    const int g0 = c * cg, gn = min(cg, groups - g0);
     for (int li = wave; li < gn; li += 4) {
       const int gi = g0 + li;
       const int n_tok = s_n[gi];
@@ -465,6 +674,15 @@ static int launch_moe(const uint8_t* gate, const uint8_t* up, const uint8_t* dow
                       hipStream_t stream, int phases) {
   const uint8_t* stab = tables ? tables + TAB_IQ3S_SIGNED : nullptr;
   int st = OK;
+  if (phases & 8) {
+    const size_t lds = (size_t)moe_tab_bytes<KIND>() + 2 * (16 * row_bytes(KIND, FRONT_D) + 16);
+    auto kern = k_moe_front<KIND, KIND_DOWN, XT, LT, TPG>;
+    if (lds + static_lds(kern) > LDS_BYTES) return fail(E_UNSUPPORTED, "moe_decode: %zu bytes of LDS", lds);
+    hipLaunchKernelGGL(kern, dim3((unsigned)(F / 16), (unsigned)(B * K + 1)), dim3(256), lds, stream, gate, up, sg,
+                       su, logits, x, wg, (int)K, (int)B, (int)F, stab, ws);
+    st = check_launch("moe_decode front");
+    if (st) return st;
+  }
   if (phases & 1) {
     auto route = [&](auto vc) {
       constexpr int V = decltype(vc)::value;
@@ -479,17 +697,25 @@ static int launch_moe(const uint8_t* gate, const uint8_t* up, const uint8_t* dow
   }
   if (phases & 2) {
     const size_t lds = (size_t)moe_tab_bytes<KIND>() + 2 * (16 * row_bytes(KIND, D) + 16);
-    hipLaunchKernelGGL((k_moe_gate_up<KIND, KIND_DOWN, XT, TPG>), dim3((unsigned)(F / 16), (unsigned)(B * K + 1)),
-                       dim3(256), lds, stream, gate, up, sg, su, (int)E, (int)K, (int)B, (int)D, (int)F, stab, ws);
+    auto kern = k_moe_gate_up<KIND, KIND_DOWN, XT, TPG>;
+    if (lds + static_lds(kern) > LDS_BYTES) return fail(E_UNSUPPORTED, "moe_decode: %zu bytes of LDS", lds);
+    hipLaunchKernelGGL(kern, dim3((unsigned)(F / 16), (unsigned)(B * K + 1)), dim3(256), lds, stream, gate, up, sg,
+                       su, (int)E, (int)K, (int)B, (int)D, (int)F, stab, ws);
     st = check_launch("moe_decode gate_up");
     if (st) return st;
   }
   if (phases & 4) {
     const int64_t rbd = row_bytes(KIND_DOWN, F);
     const size_t slot = (size_t)(((15 + 16 * rbd + 15) >> 4) << 4);
-    const size_t lds = (size_t)moe_tab_bytes<KIND_DOWN>() + 2 * DOWN_CHUNK_G * slot;
-    hipLaunchKernelGGL((k_moe_down<KIND_DOWN, XT, TPG>), dim3((unsigned)(D / 16)), dim3(256), lds, stream, down, sd,
-                       (int)E, (int)K, (int)B, (int)D, (int)F, stab, ws, out);
+    // as many groups a chunk as two chunks' slices fit beside the kernel's own LDS
+    auto kern = k_moe_down<KIND_DOWN, XT, TPG>;
+    const size_t used = static_lds(kern) + (size_t)moe_tab_bytes<KIND_DOWN>();
+    const size_t room = used < LDS_BYTES ? LDS_BYTES - used : 0;
+    const int cg = (int)std::min<size_t>(DOWN_CHUNK_G, room / (2 * slot));
+    if (cg < 1) return fail(E_UNSUPPORTED, "moe_decode: down rows of %lld bytes", (long long)rbd);
+    const size_t lds = (size_t)moe_tab_bytes<KIND_DOWN>() + 2 * (size_t)cg * slot;
+    hipLaunchKernelGGL(kern, dim3((unsigned)(D / 16)), dim3(256), lds, stream, down, sd, (int)E, (int)K, (int)B,
+                       (int)D, (int)F, cg, stab, ws, out);
     st = check_launch("moe_decode down");
   }
   return st;
@@ -525,6 +751,10 @@ int moe_decode(int phases, int kind, int kind_down, const void* gate, const void
     return fail(E_WORKSPACE, "moe_decode: workspace of %zu bytes, %zu needed", workspace_bytes, need);
   MoeWs ws;
   moe_carve(&ws, (uint8_t*)workspace, tokens, k, d_model, d_ff, dtype_size(dtype));
+  // the common shape takes route, gate and up in one kernel (phase bit 8); the others the three-kernel path
+  if (experts == FRONT_E && d_model == FRONT_D) {
+    if (phases & 3) phases = (phases & ~3) | 8;
+  }
   const int tpg = tokens <= 4 ? 1 : tokens <= 8 ? 2 : 4;
   if (logits_dtype != F32 && logits_dtype != dtype)
     return fail(E_DTYPE, "moe_decode: logits of dtype %d with activations of %d (float32 or the same)", logits_dtype, dtype);
@@ -553,7 +783,7 @@ int moe_decode(int phases, int kind, int kind_down, const void* gate, const void
     return kind == Q2_0 ? by_down(kind_c<Q2_0>{}) : by_down(kind_c<IQ3_S>{});
   });
   if (st) return st;
-  if (!(phases & 1)) return OK;
+  if (!(phases & 9)) return OK;
   if (idx_out && hipMemcpyAsync(idx_out, ws.idx, 4 * tokens * k, hipMemcpyDeviceToDevice, (hipStream_t)stream) != hipSuccess)
     return fail(E_HIP, "moe_decode: copy of the choice failed");
   if (w_out && hipMemcpyAsync(w_out, ws.w, 4 * tokens * k, hipMemcpyDeviceToDevice, (hipStream_t)stream) != hipSuccess)

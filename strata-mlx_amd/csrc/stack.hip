@@ -16,6 +16,7 @@
 #include <type_traits>
 
 #include "launch.h"
+#include "regmac.h"
 #include "xmv.h"
 
 namespace sh {
@@ -30,185 +31,6 @@ struct StackPlan {
   int rg, kw, nw;                                          // row groups, column splits, waves (rg * kw)
   int ring_off, buf_bytes, red_off;                        // LDS byte offsets and sizes
 };
-
-// Loop-invariant decode constants held in VGPRs: a gfx9 VOP3 instruction takes no literal, so with the masks and
-// the magic in registers each pair of Q2_0 weights is one v_and_or_b32.
-struct DecodeRegs {
-  uint32_t m0, m1, m2, magic;
-};
-__device__ __forceinline__ uint32_t vreg(uint32_t c) {
-  uint32_t r;
-  asm("v_mov_b32 %0, %1" : "=v"(r) : "s"(c));
-  return r;
-}
-template <int KIND, typename MT> __device__ __forceinline__ DecodeRegs decode_regs() {
-  DecodeRegs r;
-  if constexpr (KIND == Q2_0) {
-    r.m0 = vreg(0x00030003u);
-    r.m1 = vreg(0x000C000Cu);
-    r.m2 = vreg(0x00300030u);
-    r.magic = vreg(Magic<MT>::M2);
-  } else {
-    r.m0 = r.m1 = r.m2 = 0;
-    r.magic = vreg(Magic<MT>::HI * 0x01010101u);
-  }
-  return r;
-}
-
-// a wave's activation fragments for its GPER scale groups (A operand: lane (g, n) holds row n = its token's
-// fragment g), and minus the offsets' sums for the TPG tokens of its D-rows
-template <int KIND, int TPG, int GPER> struct XRegs {
-  u32x4 xa[GPER];
-  u32x4 xb[KIND == Q2_0 ? GPER : 1];
-  float nc[GPER][TPG];
-};
-
-// XRegs for scale groups [gbase, gbase + GPER) of the matrix whose activations start at xm (row t at xm + t * cols).
-// Q2_0: lane g's fragment a takes block-local weights k = 32h + 8g + 4a + j (j < 4, h < 2) into slot 2j + h, scaled
-// by 1 / U_j (the in-place mask's unit), as XStage stages them; IQ3_S: values 8g..8g+7 of the run as they are. The
-// sums: each lane's share, added over the four lanes of a row (xor 16, 32), then fetched from a lane whose A-row is
-// the wanted token (lane 4g + t holds token g * TPG + t). Padding A-rows read token 0.
-template <int KIND, typename XT, int TPG, int GPER>
-__device__ __forceinline__ void load_x(XRegs<KIND, TPG, GPER>& X, const XT* xm, int cols, int n_tok, int gbase) {
-  using MT = XT;
-  const int lane = threadIdx.x & 63, g = lane >> 4;
-  int mt = lane_token<TPG>();
-  mt = mt < n_tok ? mt : 0;
-  const XT* xr = xm + (size_t)mt * cols;
-  float part[GPER];
-  if constexpr (KIND == Q2_0) {
-    u32x4 v[GPER][2];
-#pragma unroll
-    for (int j = 0; j < GPER; ++j) {
-      v[j][0] = *(const u32x4*)(xr + (gbase + j) * 64 + 8 * g);
-      v[j][1] = *(const u32x4*)(xr + (gbase + j) * 64 + 32 + 8 * g);
-    }
-#pragma unroll
-    for (int j = 0; j < GPER; ++j) {
-      const XT* h0 = (const XT*)&v[j][0];
-      const XT* h1 = (const XT*)&v[j][1];
-      float p = 0.0f;
-      uint32_t w[2][4];
-#pragma unroll
-      for (int a = 0; a < 2; ++a)
-#pragma unroll
-        for (int jj = 0; jj < 4; ++jj) {
-          const float inv = 1.0f / q2_unit<MT>(jj);  // a power of two: exact
-          const MT s0 = from_f32<MT>(to_f32(h0[4 * a + jj]) * inv);
-          const MT s1 = from_f32<MT>(to_f32(h1[4 * a + jj]) * inv);
-          p += (Magic<MT>::BASE + q2_unit<MT>(jj)) * (to_f32(s0) + to_f32(s1));
-          w[a][jj] = (uint32_t)__builtin_bit_cast(uint16_t, s0) | ((uint32_t)__builtin_bit_cast(uint16_t, s1) << 16);
-        }
-      X.xa[j] = u32x4{w[0][0], w[0][1], w[0][2], w[0][3]};
-      X.xb[j] = u32x4{w[1][0], w[1][1], w[1][2], w[1][3]};
-      part[j] = p;
-    }
-  } else {
-#pragma unroll
-    for (int j = 0; j < GPER; ++j) X.xa[j] = *(const u32x4*)(xr + (gbase + j) * 32 + 8 * g);
-#pragma unroll
-    for (int j = 0; j < GPER; ++j) {
-      const XT* e = (const XT*)&X.xa[j];
-      float p = 0.0f;
-#pragma unroll
-      for (int i = 0; i < 8; ++i) p += to_f32(e[i]);
-      part[j] = (Magic<MT>::BASE + 16.0f) * p;
-    }
-  }
-#pragma unroll
-  for (int j = 0; j < GPER; ++j) {
-    float p = part[j];
-    p += __shfl_xor(p, 16);
-    p += __shfl_xor(p, 32);
-#pragma unroll
-    for (int t = 0; t < TPG; ++t) X.nc[j][t] = -__shfl(p, 4 * g + t);
-  }
-}
-
-// one wave's item: its 16 rows (row n at wrow0 + n * rstride, already advanced to the wave's first group) x its
-// GPER groups. All LDS reads are issued up front; a group's scale is applied to its accumulator chain (two
-// chains, in turn) after the other chain's MFMAs. The D-rows past TPG are padding rows: their accumulators keep
-// whatever the chain left and are never used.
-template <int KIND, typename MT, int TPG, int GPER>
-__device__ __forceinline__ void item_mac(const uint8_t* wrow0, int rstride, const XRegs<KIND, TPG, GPER>& X,
-                                         const uint32_t* stab, const DecodeRegs& k, float* acc) {
-  const int lane = threadIdx.x & 63, g = lane >> 4, n = lane & 15;
-  const uint8_t* wrow = wrow0 + (size_t)n * rstride;
-  uint32_t w0[GPER], w1[GPER], dh[GPER], sc[GPER];
-  if constexpr (KIND == Q2_0) {
-#pragma unroll
-    for (int j = 0; j < GPER; ++j) {
-      const uint8_t* b = wrow + j * 18;
-      w0[j] = *(const uint16_t*)(b + 2 + 2 * g);
-      w1[j] = *(const uint16_t*)(b + 10 + 2 * g);
-      dh[j] = *(const uint16_t*)b;
-    }
-  } else {
-    uint32_t q2[GPER], qh[GPER], sg[GPER];
-#pragma unroll
-    for (int j = 0; j < GPER; ++j) {
-      const uint8_t* b = wrow + (j >> 3) * 110;
-      const int ib = j & 7;
-      q2[j] = *(const uint16_t*)(b + 2 + 8 * ib + 2 * g);
-      qh[j] = b[66 + ib];
-      sg[j] = b[74 + 4 * ib + g];
-      if (ib % 2 == 0) sc[j] = b[106 + ib / 2];
-      if (ib == 0) dh[j] = *(const uint16_t*)b;
-    }
-#pragma unroll
-    for (int j = 0; j < GPER; ++j) {
-      const uint32_t h = qh[j] >> (2 * g);
-      w0[j] = stab[(q2[j] & 0xffu) | ((h & 1u) << 8) | ((sg[j] & 15u) << 9)];
-      w1[j] = stab[(q2[j] >> 8) | ((h & 2u) << 7) | ((sg[j] >> 4) << 9)];
-    }
-  }
-  f32x4 D[2] = {{0.0f, 0.0f, 0.0f, 0.0f}, {0.0f, 0.0f, 0.0f, 0.0f}};
-  float dprev = 0.0f;
-#pragma unroll
-  for (int j = 0; j < GPER; ++j) {
-    f32x4& Dj = D[j & 1];
-#pragma unroll
-    for (int t = 0; t < TPG; ++t) Dj[t] = X.nc[j][t];
-    if constexpr (KIND == Q2_0) {
-      const uint32_t W = w0[j] | (w1[j] << 16), W8 = W >> 8;
-      u32x4 fa, fb;
-      fa.x = (W & k.m0) | k.magic;
-      fa.y = (W & k.m1) | k.magic;
-      fa.z = (W & k.m2) | k.magic;
-      fb.x = (W8 & k.m0) | k.magic;
-      fb.y = (W8 & k.m1) | k.magic;
-      fb.z = (W8 & k.m2) | k.magic;
-      if constexpr (std::is_same_v<MT, bf16>) {  // bit 7 of a bf16 half is exponent: code 3 shifted down
-        fa.w = ((W >> 6) & k.m0) | k.magic;
-        fb.w = ((W >> 14) & k.m0) | k.magic;
-      } else {
-        fa.w = (W & (k.m2 << 2)) | k.magic;
-        fb.w = (W8 & (k.m2 << 2)) | k.magic;
-      }
-      Dj = mfma<MT>(X.xa[j], fa, Dj);
-      Dj = mfma<MT>(X.xb[j], fb, Dj);
-    } else {
-      u32x4 fw;
-      fw.x = __builtin_amdgcn_perm(k.magic, w0[j], 0x04010400u);
-      fw.y = __builtin_amdgcn_perm(k.magic, w0[j], 0x04030402u);
-      fw.z = __builtin_amdgcn_perm(k.magic, w1[j], 0x04010400u);
-      fw.w = __builtin_amdgcn_perm(k.magic, w1[j], 0x04030402u);
-      Dj = mfma<MT>(X.xa[j], fw, Dj);
-    }
-    if (j > 0) {  // the previous group, on the other chain
-#pragma unroll
-      for (int t = 0; t < TPG; ++t) acc[t] = fmaf(dprev, D[(j - 1) & 1][t], acc[t]);
-    }
-    if constexpr (KIND == Q2_0) {
-      dprev = half_bits(dh[j]);
-    } else {
-      const int ib = j & 7;
-      dprev = half_bits(dh[j & ~7]) * (float)(1 + 2 * ((sc[j & ~1] >> (4 * (ib & 1))) & 15u));
-    }
-  }
-#pragma unroll
-  for (int t = 0; t < TPG; ++t) acc[t] = fmaf(dprev, D[(GPER - 1) & 1][t], acc[t]);
-}
 
 template <int KIND, typename XT, int TPG, int GPER, int NWMAX>
 __global__ __launch_bounds__(NWMAX * 64) void k_stack_mv(const uint8_t* __restrict__ blocks, StackPlan P,

@@ -86,3 +86,77 @@ def test_repeated_calls_reuse_the_workspace(tables, dev):
     first = moe(logits, x)
     for _ in range(5):
         assert torch.equal(moe(logits, x), first)
+
+
+@pytest.fixture(scope="module")
+def c3_layers(tables, dev):
+    """The benchmark's layer shape (512 experts, d 2048, ffn 512), blocks made on the GPU: Q2_0, IQ3_S, and IQ3_S
+    gate/up with Q2_0 down. The oracle fetches the chosen experts' bytes back."""
+    E, D, F = 512, 2048, 512
+    out = {}
+    for n_k, kinds in enumerate((("Q2_0", "Q2_0"), ("IQ3_S", "IQ3_S"), ("IQ3_S", "Q2_0"))):
+        kd = {"gate": kinds[0], "up": kinds[0], "down": kinds[1], "sgate": kinds[0], "sup": kinds[0],
+              "sdown": kinds[1]}
+        rc = {"gate": (E * F, D), "up": (E * F, D), "down": (E * D, F), "sgate": (F, D), "sup": (F, D),
+              "sdown": (D, F)}
+        shapes = {"gate": (E, F, D), "up": (E, F, D), "down": (E, D, F), "sgate": (1, F, D), "sup": (1, F, D),
+                  "sdown": (1, D, F)}
+        # IQ3_S weights reach 465 times their block scale: its smaller scales keep float16 products finite
+        raw = {n: synth.random_blocks_gpu(kd[n], *rc[n], 40 + 10 * n_k + i, dev,
+                                          sigma=0.0005 if kd[n] == "IQ3_S" else 0.01)
+               for i, n in enumerate(rc)}
+        lin = {n: SB.BlockSwitchLinear(raw[n], kd[n], shapes[n]) for n in raw}
+        shared = tuple(OB.dequantize(raw[n].cpu().numpy(), kd[n], shapes[n], tables) for n in ("sgate", "sup", "sdown"))
+
+        def fetcher(name, rows, cols, kind, stacks=raw):
+            per = rows * OB.row_bytes(kind, cols)
+            return lambda e: stacks[name][e * per:(e + 1) * per].cpu().numpy()
+
+        fetch = (fetcher("gate", F, D, kinds[0]), fetcher("up", F, D, kinds[0]), fetcher("down", D, F, kinds[1]))
+        out[kinds] = (fetch, lin, shared)
+    return out
+
+
+@pytest.mark.parametrize("kinds, tokens, dtype", [
+    (("Q2_0", "Q2_0"), 1, torch.bfloat16), (("Q2_0", "Q2_0"), 4, torch.bfloat16),
+    (("Q2_0", "Q2_0"), 8, torch.bfloat16), (("Q2_0", "Q2_0"), 16, torch.bfloat16),
+    (("Q2_0", "Q2_0"), 2, torch.float16), (("IQ3_S", "IQ3_S"), 1, torch.bfloat16),
+    (("IQ3_S", "IQ3_S"), 8, torch.bfloat16), (("IQ3_S", "IQ3_S"), 3, torch.float16),
+    (("IQ3_S", "Q2_0"), 5, torch.bfloat16)])
+def test_the_benchmark_shape_is_the_oracles_block(kinds, tokens, dtype, c3_layers, tables, dev):
+    """512 experts, d 2048: route, gate and up in one kernel, then down and the combine."""
+    E, D, F, K = 512, 2048, 512, 10
+    fetch, lin, shared = c3_layers[kinds]
+    rng = np.random.default_rng(tokens + 100)
+    name = "bfloat16" if dtype == torch.bfloat16 else "float16"
+    x = torch.from_numpy(rng.standard_normal((tokens, D)).astype(np.float32)).to(dtype)
+    logits = torch.from_numpy(rng.standard_normal((tokens, E)).astype(np.float32)).to(dtype)
+    if tokens >= 4:
+        logits[2] = logits[0]  # tokens sharing their whole choice
+    wg = torch.from_numpy(rng.standard_normal(D).astype(np.float32) * 0.05).to(dtype)
+    moe = SF.MoEDecode(lin["gate"], lin["up"], lin["down"], lin["sgate"], lin["sup"], lin["sdown"], wg.to(dev), K)
+    out, idx, wt = moe(logits.to(dev), x.to(dev), want_choice=True)
+    want, want_idx, want_w = OM.moe_decode_blocks(logits.float().numpy(), x.float().numpy(), K, fetch, kinds,
+                                                  (E, D, F), shared, wg.float().numpy(), tables, name)
+    np.testing.assert_array_equal(idx.cpu().numpy(), want_idx)
+    np.testing.assert_allclose(wt.cpu().numpy(), want_w, rtol=2e-6, atol=1e-7)
+    assert np.isfinite(want).all()
+    assert rel_err(out.float().cpu(), want) <= 1e-2
+
+
+def test_the_benchmark_shape_with_float32_logits(c3_layers, tables, dev):
+    E, D, F, K = 512, 2048, 512, 10
+    fetch, lin, shared = c3_layers[("Q2_0", "Q2_0")]
+    rng = np.random.default_rng(7)
+    x = torch.from_numpy(rng.standard_normal((8, D)).astype(np.float32)).to(torch.bfloat16)
+    logits = torch.from_numpy(rng.standard_normal((8, E)).astype(np.float32))
+    logits[:, 5] = logits[:, 9]  # exact ties go to the lower index
+    wg = torch.from_numpy(rng.standard_normal(D).astype(np.float32) * 0.05).to(torch.bfloat16)
+    moe = SF.MoEDecode(lin["gate"], lin["up"], lin["down"], lin["sgate"], lin["sup"], lin["sdown"], wg.to(dev), K)
+    out, idx, wt = moe(logits.to(dev), x.to(dev), want_choice=True)
+    want, want_idx, _ = OM.moe_decode_blocks(logits.numpy(), x.float().numpy(), K, fetch, ("Q2_0", "Q2_0"),
+                                             (E, D, F), shared, wg.float().numpy(), tables, "bfloat16")
+    np.testing.assert_array_equal(idx.cpu().numpy(), want_idx)
+    assert rel_err(out.float().cpu(), want) <= 1e-2
+    for _ in range(3):  # the workspace reused: the same bits
+        assert torch.equal(moe(logits.to(dev), x.to(dev)), out)
