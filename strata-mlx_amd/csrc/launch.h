@@ -77,4 +77,37 @@ template <typename K> inline size_t static_lds(K* kern) {
   return attr.sharedSizeBytes;
 }
 
+// compute units of the current device
+inline int device_cus() {
+  static int cus = 0;
+  if (!cus) {
+    int dev = 0;
+    (void)hipGetDevice(&dev);
+    (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+    if (cus <= 0) cus = 256;
+  }
+  return cus;
+}
+
+// the LDS row stride of rows of rbytes: padded by 16-byte chunks so 16 consecutive rows start in distinct
+// 4-bank windows of the 64 banks, where the row is whole chunks and the blocks are 16-byte aligned
+inline void row_layout(int64_t rbytes, bool aligned, int& rstride, int& padded) {
+  padded = 0;
+  rstride = (int)rbytes;
+  if (rbytes % 16 || !aligned) return;
+  for (int pad = 0; pad <= 48; pad += 16) {
+    const int dw = (int)(rbytes + pad) / 4;
+    bool distinct = true;
+    for (int a = 0; a < 16 && distinct; ++a)
+      for (int b = a + 1; b < 16 && distinct; ++b) distinct = ((a * dw) % 64) / 4 != ((b * dw) % 64) / 4;
+    if (distinct) {
+      rstride = (int)rbytes + pad;
+      padded = 1;
+      return;
+    }
+  }
+  rstride = (int)rbytes + 16;
+  padded = 1;
+}
+
 }  // namespace sh

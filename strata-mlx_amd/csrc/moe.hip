@@ -42,7 +42,9 @@ struct MoeWs {
   float* w;           // [B][k]
   float* gsh;         // [B]: the shared expert's gate logit, rounded to the activation type
   uint8_t* xp;        // [B][D]: the hidden states staged for gate/up's kind (xmv.h stage_index)
-  uint8_t* h;         // [B*k + B][F]: swiglu(gate, up), staged for down's kind
+  uint8_t* h;         // [B*k + B][F]: swiglu(gate, up), staged for down's kind (natural order in the two-kernel path)
+  float* y;           // [B*k + B][D]: each pair's down outputs, rounded to the activation type (two-kernel path)
+  int32_t* cnt;       // [D / 64]: the tail's finished blocks a row tile, zero between calls
 };
 
 static inline size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
@@ -65,6 +67,8 @@ static size_t moe_carve(MoeWs* ws, uint8_t* base, int64_t B, int64_t k, int64_t 
   w.gsh = (float*)take(4 * B);
   w.xp = take((size_t)B * D * es);
   w.h = take((size_t)P * F * es);
+  w.y = (float*)take((size_t)4 * P * D);
+  w.cnt = (int32_t*)take((size_t)4 * (D / 64 + 1));
   if (ws) *ws = w;
   return off;
 }
@@ -291,77 +295,115 @@ __global__ __launch_bounds__(256) void k_moe_gate_up(const uint8_t* __restrict__
   }
 }
 
-// ---- route, gate and up in one kernel, for the common shape (512 experts, d_model 2048)
+// ---- the common shape (512 experts, d_model 2048, expert width 512): two kernels
 //
-// Every block routes the whole window again (B tokens' top-k of 512 logits: a few microseconds of arithmetic on
-// data in L2), so no kernel boundary stands between the choice and the expert products. The groups are the chosen
-// experts in ascending order, then the shared expert; block (x, g) takes 16 rows of gate and up of group g. Its
-// weights are staged in LDS and its tokens' activation fragments loaded into registers straight from x in the same
-// memory trip; block (0, 0) also writes the group table, the choice and its weights for the down kernel, block
-// (1, 0) the shared expert's gate logits.
+// front  route, gate and up with SwiGLU. A block of 8 waves routes the whole window itself (a wave a token: its
+//        top-k of the 512 logits), so no kernel boundary stands between the choice and the expert products, then
+//        streams a contiguous run of the items (group g, row tile r): 16 rows of gate and 16 of up of the group's
+//        expert. The groups are the chosen experts in ascending order, then the shared expert. Items go through an
+//        LDS ring filled by direct loads, NBUF - 1 in flight while one is multiplied; wave q multiplies the 16 rows
+//        of gate and of up over column eighth q with the group's activation fragments in registers (loaded as
+//        they are: the Q2_0 decode shifts each code down itself). The epilogue rounds gate and up to
+//        the activation type and writes swiglu(gate, up) per pair, in natural order. Block 0 also writes the
+//        choice, its weights and the group table and clears the tail's counters; block 1 the shared expert's gate
+//        logits.
+// tail   down and the combine. Block (tile, g) multiplies 64 rows of down of group g's expert (a wave 16 rows,
+//        all 512 columns) and writes each pair's outputs, rounded to the activation type, to the workspace; the
+//        last block of a row tile to finish (a counter per tile) combines the tile for every token.
 
-constexpr int FRONT_E = 512, FRONT_D = 2048;
+constexpr int FRONT_E = 512, FRONT_D = 2048, FRONT_F = 512;
+constexpr int FRONT_WAVES = 8, FRONT_LMAX = 6;
+constexpr int TAIL_ROWS = 64;  // rows of down a tail block
 
-template <int KIND, int KIND_DOWN, typename XT, typename LT, int TPG>
-__global__ __launch_bounds__(256) void k_moe_front(const uint8_t* __restrict__ gate, const uint8_t* __restrict__ up,
-                                                   const uint8_t* __restrict__ sh_gate, const uint8_t* __restrict__ sh_up,
-                                                   const LT* __restrict__ logits, const XT* __restrict__ x,
-                                                   const XT* __restrict__ wgt, int K, int B, int F,
-                                                   const uint8_t* __restrict__ signed_tab, MoeWs ws) {
+struct FrontPlan {
+  int rstride;    // LDS bytes a row (padded so a wave's 16 rows fall in distinct banks)
+  int loads;      // direct loads a thread an item
+  int nbuf;       // ring slots
+  int buf_bytes;  // bytes a slot
+  int ring_off;   // after the IQ3_S table
+  int red_off;    // [2][7][64][TPG] floats: gate's and up's partial sums of waves 1..7
+};
+
+template <int KIND, typename XT, typename LT, int TPG>
+__global__ __launch_bounds__(FRONT_WAVES * 64) void k_moe_front(
+    const uint8_t* __restrict__ gate, const uint8_t* __restrict__ up, const uint8_t* __restrict__ sh_gate,
+    const uint8_t* __restrict__ sh_up, const LT* __restrict__ logits, const XT* __restrict__ x,
+    const XT* __restrict__ wgt, int K, int B, FrontPlan fp, const uint8_t* __restrict__ signed_tab, MoeWs ws) {
   using MT = XT;
   using RK = RouteKey<LT>;
   using key_t = typename RK::type;
-  constexpr int E = FRONT_E, D = FRONT_D, VPL = E / 64, WORDS = E / 32;
-  constexpr int GPER = KIND == Q2_0 ? D / 64 / 4 : D / 32 / 4;  // a wave's quarter of the scale groups
+  constexpr int E = FRONT_E, D = FRONT_D, F = FRONT_F, VPL = E / 64, WORDS = E / 32, TILES = F / 16;
+  constexpr int NT = FRONT_WAVES * 64;
+  constexpr int GPER = KIND == Q2_0 ? D / 64 / FRONT_WAVES : D / 32 / FRONT_WAVES;  // a wave's eighth of the groups
   constexpr int RB = (int)row_bytes_dev(KIND, D);
+  constexpr int CPR_SRC = RB / 16;
+  extern __shared__ u32x4 dyn[];
+  uint8_t* lds = (uint8_t*)dyn;
+  const uint32_t lds_base = SH_LDS_ADDR(dyn);
+  float* red = (float*)(lds + fp.red_off);
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int row0 = blockIdx.x * 16, gy = blockIdx.y;
+  const int kq = wave;
   const int P = B * K;
   __shared__ int s_idx[MOE_MAX_PAIRS];
   __shared__ float s_wt[MOE_MAX_PAIRS];
   __shared__ uint32_t s_flag[WORDS];
-  __shared__ int s_cnt[MOE_MAX_PAIRS + 1];
-  __shared__ int s_e, s_groups, s_n, s_pair[16];
-  __shared__ float s_red[2][4][64][TPG];
-  extern __shared__ u32x4 dyn[];
-  uint8_t* tab = (uint8_t*)dyn;
-  uint8_t* wgl = tab + moe_tab_bytes<KIND>();
-  uint8_t* wul = wgl + 16 * RB + 16;
+  __shared__ int s_gexp[MOE_MAX_PAIRS + 1];
+  __shared__ int s_groups;
+  __shared__ int s_wp[FRONT_WAVES][16];
 
-  if (tid < WORDS) s_flag[tid] = 0u;
-  if (tid <= MOE_MAX_PAIRS) s_cnt[tid] = 0;
-  // 1. each token's top-k of the logits and the softmax of the chosen (a wave a token)
-  for (int t = wave; t < B; t += 4) {
-    key_t key[VPL];
+  // the IQ3_S table first: it does not wait on the choice (2048 chunks, four a thread)
+  if constexpr (KIND == IQ3_S) {
 #pragma unroll
-    for (int i = 0; i < VPL; ++i) key[i] = RK::make(logits[(int64_t)t * E + i * 64 + lane], i * 64 + lane);
-    float top = 0.0f, sum = 0.0f, my_e = 0.0f;
-    for (int r = 0; r < K; ++r) {
-      key_t best = key[0];
-#pragma unroll
-      for (int i = 1; i < VPL; ++i) best = key[i] > best ? key[i] : best;
-      best = RK::wave_max(best);
-      const float v = RK::value(best);
-      if (r == 0) top = v;
-      const float ev = expf(v - top);
-      sum += ev;
-      if (lane == r) {
-        my_e = ev;
-        s_idx[t * K + r] = RK::index(best);
-      }
-#pragma unroll
-      for (int i = 0; i < VPL; ++i)
-        if (key[i] == best) key[i] = 0;
+    for (int i = 0; i < IQ3S_SIGNED_BYTES / 16 / NT; ++i) {
+      const int c0 = wave * 64 + i * NT;
+      lds_dma16(signed_tab, 16 * (c0 + lane), lds_base + 16 * c0);
     }
-    if (lane < K) s_wt[t * K + lane] = my_e / sum;
+  }
+  if (tid < WORDS) s_flag[tid] = 0u;
+
+  // 1. each token's top-k of the logits and the softmax of the chosen (a wave a token, its logits loaded first)
+  {
+    key_t key[2][VPL];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int t = wave + FRONT_WAVES * u;
+      if (t < B) {
+#pragma unroll
+        for (int i = 0; i < VPL; ++i) key[u][i] = RK::make(logits[(int64_t)t * E + i * 64 + lane], i * 64 + lane);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int t = wave + FRONT_WAVES * u;
+      if (t >= B) break;
+      float top = 0.0f, sum = 0.0f, my_e = 0.0f;
+      for (int r = 0; r < K; ++r) {
+        key_t best = key[u][0];
+#pragma unroll
+        for (int i = 1; i < VPL; ++i) best = key[u][i] > best ? key[u][i] : best;
+        best = RK::wave_max(best);
+        const float v = RK::value(best);
+        if (r == 0) top = v;
+        const float ev = expf(v - top);
+        sum += ev;
+        if (lane == r) {
+          my_e = ev;
+          s_idx[t * K + r] = RK::index(best);
+        }
+#pragma unroll
+        for (int i = 0; i < VPL; ++i)
+          if (key[u][i] == best) key[u][i] = 0;
+      }
+      if (lane < K) s_wt[t * K + lane] = my_e / sum;
+    }
   }
   __syncthreads();
   if (tid < P) atomicOr(&s_flag[s_idx[tid] >> 5], 1u << (s_idx[tid] & 31));
   __syncthreads();
-  // 2. this block's group: the gy-th chosen expert in ascending order, or the shared expert after them
+  // 2. the groups: the chosen experts in ascending order, then the shared expert
   if (wave == 0) {
-    const uint32_t word = lane < WORDS ? s_flag[lane] : 0u;
+    uint32_t word = lane < WORDS ? s_flag[lane] : 0u;
     const int cnt = __popc(word);
     int incl = cnt;
 #pragma unroll
@@ -369,46 +411,30 @@ __global__ __launch_bounds__(256) void k_moe_front(const uint8_t* __restrict__ g
       const int v = __shfl_up(incl, o);
       if (lane >= o) incl += v;
     }
-    const int total = __shfl(incl, 63), excl = incl - cnt;
-    if (lane == 0) s_groups = total + 1;
-    if (gy >= excl && gy < incl) {
-      uint32_t w = word;
-      for (int i = 0; i < gy - excl; ++i) w &= w - 1u;
-      s_e = lane * 32 + __ffs(w) - 1;
+    const int total = __shfl(incl, 63);
+    int pos = incl - cnt;
+    while (word) {
+      s_gexp[pos++] = lane * 32 + __ffs(word) - 1;
+      word &= word - 1u;
     }
-    if (lane == 0 && gy == total) s_e = E;
+    if (lane == 0) {
+      s_gexp[total] = E;
+      s_groups = total + 1;
+    }
   }
   __syncthreads();
   const int groups = s_groups;
-
-  // block (0, 0): the group table, the choice and its weights, for the down kernel and the caller
-  if (blockIdx.x == 0 && gy == 0) {
-    int g_p = 0, rank = 0, e_p = 0;
+  if (blockIdx.x == 0) {  // the choice, its weights and the groups' experts for the tail and the caller
     if (tid < P) {
-      e_p = s_idx[tid];
-      const int w = e_p >> 5;
-      for (int i = 0; i < w; ++i) g_p += __popc(s_flag[i]);
-      g_p += __popc(s_flag[w] & ((1u << (e_p & 31)) - 1u));
-      rank = atomicAdd(&s_cnt[g_p], 1);  // order within a group: any (each token's rows are its own)
-      ws.g_pair[g_p * 16 + rank] = tid;
-      ws.idx[tid] = e_p;
+      ws.idx[tid] = s_idx[tid];
       ws.w[tid] = s_wt[tid];
     }
-    __syncthreads();
-    if (tid < P && rank == 0) {
-      ws.g_expert[g_p] = e_p;
-      ws.g_ntok[g_p] = s_cnt[g_p];
-    }
-    if (tid == 0) {
-      ws.g_expert[groups - 1] = E;
-      ws.g_ntok[groups - 1] = B;
-      *ws.n_groups = groups;
-    }
-    if (tid < B) ws.g_pair[(groups - 1) * 16 + tid] = P + tid;
+    if (tid < groups) ws.g_expert[tid] = s_gexp[tid];
+    if (tid < D / TAIL_ROWS) ws.cnt[tid] = 0;
+    if (tid == 0) *ws.n_groups = groups;
   }
-  // block (1, 0): the shared expert's gate logit of each token, rounded to the activation type
-  if (blockIdx.x == 1 && gy == 0) {
-    for (int t = wave; t < B; t += 4) {
+  if (blockIdx.x == 1 % gridDim.x) {  // the shared expert's gate logit of each token, rounded to the activation type
+    for (int t = wave; t < B; t += FRONT_WAVES) {
       float acc = 0.0f;
 #pragma unroll
       for (int j = 0; j < D / 512; ++j) {
@@ -423,79 +449,256 @@ __global__ __launch_bounds__(256) void k_moe_front(const uint8_t* __restrict__ g
       if (lane == 0) ws.gsh[t] = to_f32(from_f32<XT>(acc));
     }
   }
-  if (gy >= groups) return;  // block-uniform: no more barriers for these blocks
-  const int e = s_e;
-  // 3. the group's pairs in token order (a token chooses an expert at most once)
-  if (wave == 0) {
-    int j_hit = -1;
-    if (e < E && lane < B)
-      for (int j = 0; j < K; ++j)
-        if (s_idx[lane * K + j] == e) j_hit = j;
-    const uint64_t bal = __ballot(j_hit >= 0);
-    if (e < E) {
-      if (j_hit >= 0) s_pair[__popcll(bal & ((1ull << lane) - 1ull))] = lane * K + j_hit;
-      if (lane == 0) s_n = __popcll(bal);
-    } else {
-      if (lane < B) s_pair[lane] = P + lane;
-      if (lane == 0) s_n = B;
-    }
+
+  // 3. this block's run of the items
+  const int items = groups * TILES;
+  const int per = (items + gridDim.x - 1) / gridDim.x;
+  const int first = blockIdx.x * per, last = min(items, first + per);
+  if (first >= last) return;  // block-uniform
+
+  // this thread's chunks of an item: matrix (0 gate, 1 up) and byte offset from the item's first row; the slot's
+  // tail past the two matrices re-reads up's last chunk
+  const int cpr = fp.rstride >> 4;
+  int pre_off[FRONT_LMAX];
+  bool pre_up[FRONT_LMAX];
+#pragma unroll
+  for (int j = 0; j < FRONT_LMAX; ++j) {
+    const int s = (j * FRONT_WAVES + wave) * 64 + lane;
+    const int m = s / (16 * cpr), rem = s - m * 16 * cpr;
+    const int row = rem / cpr, kk = rem - row * cpr;
+    pre_up[j] = m >= 1;
+    pre_off[j] = m >= 2 ? 15 * RB + 16 * (CPR_SRC - 1) : row * RB + 16 * min(kk, CPR_SRC - 1);
   }
-  __syncthreads();
-  const int n_tok = s_n;
-  // 4. weights to LDS and activation fragments to registers, in one memory trip
   const int64_t ebytes = (int64_t)F * RB;
-  const uint8_t* g_src = (e == E ? sh_gate : gate + (int64_t)e * ebytes) + (int64_t)row0 * RB;
-  const uint8_t* u_src = (e == E ? sh_up : up + (int64_t)e * ebytes) + (int64_t)row0 * RB;
-  ByteStage<8> wst(wgl, g_src, 16 * RB, wul, u_src, 16 * RB);
-  wst.load(0, tid, 256);
-  int mt = lane_token<TPG>();
-  mt = mt < n_tok ? mt : 0;
-  const int pp = s_pair[mt];
-  const XT* xr = x + (int64_t)(pp < P ? pp / K : pp - P) * D;
-  XRegs<KIND, TPG, GPER> X;
-  load_x_row<KIND, XT, TPG, GPER>(X, xr, wave * GPER);
-  wst.store(0, tid, 256);
-  for (int p2 = 1; p2 < wst.passes(256); ++p2) {
-    wst.load(p2, tid, 256);
-    wst.store(p2, tid, 256);
-  }
-  if constexpr (KIND == IQ3_S) {
-    ByteStage<8> tst(tab, signed_tab, IQ3S_SIGNED_BYTES, nullptr, nullptr, 0);
-    for (int p2 = 0; p2 < tst.passes(256); ++p2) {
-      tst.load(p2, tid, 256);
-      tst.store(p2, tid, 256);
-    }
-  }
-  __syncthreads();
-  // 5. this wave's quarter of the columns of gate and of up
+  auto issue = [&](int item) {
+    const int g = item / TILES, r = item - g * TILES;
+    const int e = s_gexp[g];
+    const uint8_t* gs = (e == E ? sh_gate : gate + (int64_t)e * ebytes) + (int64_t)r * 16 * RB;
+    const uint8_t* us = (e == E ? sh_up : up + (int64_t)e * ebytes) + (int64_t)r * 16 * RB;
+    const uint32_t buf = lds_base + fp.ring_off + (item % fp.nbuf) * fp.buf_bytes + wave * 1024;
+#pragma unroll
+    for (int j = 0; j < FRONT_LMAX; ++j)
+      if (j < fp.loads) lds_dma16p((pre_up[j] ? us : gs) + pre_off[j], buf + j * (NT * 16));
+  };
+  for (int k = 0; k < fp.nbuf - 1 && first + k < last; ++k) issue(first + k);
+
   const DecodeRegs kr = decode_regs<KIND, MT>();
-  const int wcol = KIND == Q2_0 ? wave * GPER * 18 : (wave * GPER / 8) * 110;
-  float acc_g[TPG], acc_u[TPG];
+  XRegs<KIND, TPG, GPER> X;
+  const int wcol = KIND == Q2_0 ? kq * GPER * 18 : (kq * GPER / 8) * 110;  // the wave's first group in a row
+  constexpr int RED = 7 * 64 * TPG;  // up's partial sums after gate's
+  // an item's results are stored at the start of the next (after that item's wait: see the streaming matvec)
+  XT hv[TPG];
+  int hp[TPG], hrow = -1;
+  auto store_h = [&]() {
+    if (wave == 0 && hrow >= 0) {
 #pragma unroll
-  for (int i = 0; i < TPG; ++i) acc_g[i] = acc_u[i] = 0.0f;
-  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-  item_mac<KIND, MT, TPG, GPER>(wgl + lead_of(g_src) + wcol, RB, X, (const uint32_t*)tab, kr, acc_g);
-  item_mac<KIND, MT, TPG, GPER>(wul + lead_of(u_src) + wcol, RB, X, (const uint32_t*)tab, kr, acc_u);
+      for (int t = 0; t < TPG; ++t)
+        if (hp[t] >= 0) ((XT*)ws.h)[(int64_t)hp[t] * F + hrow] = hv[t];
+    }
+  };
+  int g_cur = -1, n_tok = 0;
+  for (int item = first; item < last; ++item) {
+    const int ahead = min(fp.nbuf - 2, last - 1 - item);  // items issued after this one
+    wait_vmcnt(ahead * fp.loads);
+    lds_sync();  // this item is in LDS for every wave; every wave is done with the item before
+    store_h();
+    if (item + fp.nbuf - 1 < last) issue(item + fp.nbuf - 1);
+    const int g = item / TILES, r = item - g * TILES;
+    if (g != g_cur) {  // a new group: its tokens in token order (each wave for itself), their fragments
+      g_cur = g;
+      const int e = s_gexp[g];
+      if (e < E) {
+        int jh = -1;
+        if (lane < B)
+          for (int j = 0; j < K; ++j)
+            if (s_idx[lane * K + j] == e) jh = j;
+        const uint64_t bal = __ballot(jh >= 0);
+        n_tok = __popcll(bal);
+        if (jh >= 0) s_wp[wave][__popcll(bal & ((1ull << lane) - 1ull))] = lane * K + jh;
+      } else {
+        n_tok = B;
+        if (lane < B) s_wp[wave][lane] = P + lane;
+      }
+      __builtin_amdgcn_wave_barrier();
+      int mt = lane_token<TPG>();
+      mt = mt < n_tok ? mt : 0;
+      const int pp = s_wp[wave][mt];
+      load_x_row<KIND, XT, TPG, GPER, true>(X, x + (int64_t)(pp < P ? pp / K : pp - P) * D, kq * GPER);
+    }
+    float acc_g[TPG], acc_u[TPG];
 #pragma unroll
-  for (int i = 0; i < TPG; ++i) {
-    s_red[0][wave][lane][i] = acc_g[i];
-    s_red[1][wave][lane][i] = acc_u[i];
-  }
-  __syncthreads();
-  if (wave == 0) {
-    const int g = lane >> 4, n = lane & 15;
-    float scale;
-    const int at = stage_index<KIND_DOWN, XT>(row0 + n, scale);
+    for (int t = 0; t < TPG; ++t) acc_g[t] = acc_u[t] = 0.0f;
+    const uint8_t* row0 = lds + fp.ring_off + (item % fp.nbuf) * fp.buf_bytes + wcol;
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    item_mac<KIND, MT, TPG, GPER, true>(row0, fp.rstride, X, (const uint32_t*)lds, kr, acc_g);
+    item_mac<KIND, MT, TPG, GPER, true>(row0 + 16 * fp.rstride, fp.rstride, X, (const uint32_t*)lds, kr, acc_u);
+    if (wave > 0) {
 #pragma unroll
-    for (int i = 0; i < TPG; ++i) {
-      const int t = g * TPG + i;
-      if (t < n_tok) {
-        const XT gv = from_f32<XT>(s_red[0][0][lane][i] + s_red[0][1][lane][i] + s_red[0][2][lane][i] + s_red[0][3][lane][i]);
-        const XT uv = from_f32<XT>(s_red[1][0][lane][i] + s_red[1][1][lane][i] + s_red[1][2][lane][i] + s_red[1][3][lane][i]);
-        ((XT*)ws.h)[(int64_t)s_pair[t] * F + at] = from_f32<XT>(to_f32(swiglu_one(gv, uv)) * scale);
+      for (int t = 0; t < TPG; ++t) {
+        red[((wave - 1) * 64 + lane) * TPG + t] = acc_g[t];
+        red[RED + ((wave - 1) * 64 + lane) * TPG + t] = acc_u[t];
+      }
+    }
+    lds_sync();
+    if (wave == 0) {
+      const int q = lane >> 4, n = lane & 15;
+      hrow = r * 16 + n;
+#pragma unroll
+      for (int t = 0; t < TPG; ++t) {
+        const float* rd = red + lane * TPG + t;
+        float gs = acc_g[t], us = acc_u[t];
+#pragma unroll
+        for (int w = 0; w < FRONT_WAVES - 1; ++w) {
+          gs += rd[w * 64 * TPG];
+          us += rd[RED + w * 64 * TPG];
+        }
+        hv[t] = swiglu_one(from_f32<XT>(gs), from_f32<XT>(us));
+        const int tt = q * TPG + t;
+        hp[t] = tt < n_tok ? s_wp[0][tt] : -1;
       }
     }
   }
+  store_h();
+}
+
+template <int KIND, typename XT, int TPG>
+__global__ __launch_bounds__(256) void k_moe_tail(const uint8_t* __restrict__ down, const uint8_t* __restrict__ sh_down,
+                                                  int K, int B, int rstride, int loads,
+                                                  const uint8_t* __restrict__ signed_tab, MoeWs ws,
+                                                  XT* __restrict__ out) {
+#pragma clang fp contract(off)
+  using MT = XT;
+  constexpr int E = FRONT_E, D = FRONT_D, F = FRONT_F;
+  constexpr int GPER = KIND == Q2_0 ? F / 64 : F / 32;  // a wave's 16 rows whole
+  constexpr int RB = (int)row_bytes_dev(KIND, F);
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int tile = blockIdx.x, gy = blockIdx.y;
+  const int P = B * K;
+  __shared__ int s_groups, s_e, s_last;
+  __shared__ int s_idx[MOE_MAX_PAIRS];
+  __shared__ int s_wp[4][16];
+  extern __shared__ u32x4 dyn[];
+  uint8_t* lds = (uint8_t*)dyn;
+  const uint32_t lds_base = SH_LDS_ADDR(dyn);
+
+  if (tid == 0) s_groups = *ws.n_groups;
+  if (tid == 1) s_e = ws.g_expert[gy];
+  if (tid < P) s_idx[tid] = ws.idx[tid];
+  __syncthreads();
+  if (gy >= s_groups) return;  // block-uniform: past the groups the front found
+  const int e = s_e;
+  // the rows: direct loads into LDS, 16-byte chunks of the 64 rows (rstride == RB: packed from the chunk holding
+  // the first byte; padded: rows at rstride, each row's chunks re-reading its last past its end)
+  const int ring_off = KIND == IQ3_S ? IQ3S_SIGNED_BYTES : 0;
+  const uint8_t* src = (e == E ? sh_down : down + (int64_t)e * D * RB) + (int64_t)tile * TAIL_ROWS * RB;
+  {
+    const bool padded = rstride != RB;
+    const int cpr = rstride >> 4;
+    const int nb = TAIL_ROWS * RB;
+    const uint8_t* base = padded ? src : (const uint8_t*)((uintptr_t)src & ~(uintptr_t)15);
+    const int lastc = padded ? nb - 16 : ((lead_of(src) + nb - 1) & ~15);
+    for (int j = 0; j < loads; ++j) {  // loads is the same for every wave: each issues exactly `loads`
+      const int s = (j * 4 + wave) * 64 + lane;
+      int off;
+      if (padded) {
+        const int row = s / cpr, kk = s - row * cpr;
+        off = row * RB + 16 * min(kk, RB / 16 - 1);
+      } else {
+        off = 16 * s;
+      }
+      lds_dma16(base, min(off, lastc), lds_base + ring_off + (j * 4 + wave) * 1024);
+    }
+  }
+  if constexpr (KIND == IQ3_S) {
+#pragma unroll
+    for (int i = 0; i < IQ3S_SIGNED_BYTES / 16 / 256; ++i) {
+      const int c0 = wave * 64 + i * 256;
+      lds_dma16(signed_tab, 16 * (c0 + lane), lds_base + 16 * c0);
+    }
+  }
+  // the group's tokens (each wave for itself) and their fragments of h
+  int n_tok;
+  if (e < E) {
+    int jh = -1;
+    if (lane < B)
+      for (int j = 0; j < K; ++j)
+        if (s_idx[lane * K + j] == e) jh = j;
+    const uint64_t bal = __ballot(jh >= 0);
+    n_tok = __popcll(bal);
+    if (jh >= 0) s_wp[wave][__popcll(bal & ((1ull << lane) - 1ull))] = lane * K + jh;
+  } else {
+    n_tok = B;
+    if (lane < B) s_wp[wave][lane] = P + lane;
+  }
+  __builtin_amdgcn_wave_barrier();
+  int mt = lane_token<TPG>();
+  mt = mt < n_tok ? mt : 0;
+  XRegs<KIND, TPG, GPER> X;
+  load_x_row<KIND, XT, TPG, GPER, true>(X, (const XT*)ws.h + (int64_t)s_wp[wave][mt] * F, 0);
+  const DecodeRegs kr = decode_regs<KIND, MT>();
+  wait_vmcnt(0);
+  lds_sync();
+  float acc[TPG];
+#pragma unroll
+  for (int t = 0; t < TPG; ++t) acc[t] = 0.0f;
+  const uint8_t* row0 = lds + ring_off + (rstride != RB ? 0 : lead_of(src)) + wave * 16 * rstride;
+  item_mac<KIND, MT, TPG, GPER, true>(row0, rstride, X, (const uint32_t*)lds, kr, acc);
+  // each pair's 16 outputs of this wave, rounded to the activation type
+  {
+    const int q = lane >> 4, n = lane & 15;
+    const int row = tile * TAIL_ROWS + wave * 16 + n;
+#pragma unroll
+    for (int t = 0; t < TPG; ++t) {
+      const int tt = q * TPG + t;
+      if (tt < n_tok)
+        __hip_atomic_store(&ws.y[(int64_t)s_wp[wave][tt] * D + row], to_f32(from_f32<XT>(acc[t])), __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
+  // The last block of the tile to count itself combines it. The outputs go out as device-scope stores (written
+  // through the XCD's L2) and are complete (vmcnt 0) before the count; the combining block reads them with
+  // device-scope loads after it. No device-wide fence: its L2 write-back and invalidation serialize the tile's
+  // blocks on each XCD's L2.
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  if (tid == 0)
+    s_last = __hip_atomic_fetch_add(&ws.cnt[tile], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == s_groups - 1;
+  __syncthreads();
+  if (!s_last) return;
+  // the combine (strata_mlx/fused.py:448-462): experts in 8 rows j taking k = j, j + 8, ..., each product rounded
+  for (int qv = tid; qv < B * TAIL_ROWS; qv += 256) {
+    const int t = qv / TAIL_ROWS, row = tile * TAIL_ROWS + qv % TAIL_ROWS;
+    float yv[16], wv[16];  // k <= 16
+#pragma unroll
+    for (int kk = 0; kk < 16; ++kk) {
+      yv[kk] = kk < K ? __hip_atomic_load(&ws.y[(int64_t)(t * K + kk) * D + row], __ATOMIC_RELAXED,
+                                          __HIP_MEMORY_SCOPE_AGENT) : 0.0f;
+      wv[kk] = kk < K ? ws.w[t * K + kk] : 0.0f;
+    }
+    const float ys = __hip_atomic_load(&ws.y[(int64_t)(P + t) * D + row], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    float acc2 = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      if (j < K) {
+        float part = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+          const int kk = j + 8 * i;
+          if (kk < K) {
+            const float prod = yv[kk] * wv[kk];
+            part = prod + part;
+          }
+        }
+        acc2 = j == 0 ? part : part + acc2;
+      }
+    }
+    const XT routed = from_f32<XT>(acc2);
+    const XT gate = from_f32<XT>(1.0f / (1.0f + expf(-ws.gsh[t])));
+    const XT shared = from_f32<XT>(to_f32(gate) * ys);
+    out[(int64_t)t * D + row] = from_f32<XT>(to_f32(routed) + to_f32(shared));
+  }
+  if (tid == 0) __hip_atomic_store(&ws.cnt[tile], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // ---- down and the combine: a block is 16 output rows of every group's expert
@@ -674,13 +877,50 @@ static int launch_moe(const uint8_t* gate, const uint8_t* up, const uint8_t* dow
                       hipStream_t stream, int phases) {
   const uint8_t* stab = tables ? tables + TAB_IQ3S_SIGNED : nullptr;
   int st = OK;
-  if (phases & 8) {
-    const size_t lds = (size_t)moe_tab_bytes<KIND>() + 2 * (16 * row_bytes(KIND, FRONT_D) + 16);
-    auto kern = k_moe_front<KIND, KIND_DOWN, XT, LT, TPG>;
-    if (lds + static_lds(kern) > LDS_BYTES) return fail(E_UNSUPPORTED, "moe_decode: %zu bytes of LDS", lds);
-    hipLaunchKernelGGL(kern, dim3((unsigned)(F / 16), (unsigned)(B * K + 1)), dim3(256), lds, stream, gate, up, sg,
-                       su, logits, x, wg, (int)K, (int)B, (int)F, stab, ws);
+  if (phases & 8) {  // front: route, gate and up (the common shape)
+    FrontPlan fp;
+    const int64_t rb = row_bytes(KIND, FRONT_D);
+    int padded = 0;
+    row_layout(rb, true, fp.rstride, padded);
+    const int nt = FRONT_WAVES * 64;
+    fp.loads = (int)((2 * 16 * (fp.rstride / 16) + nt - 1) / nt);
+    fp.buf_bytes = fp.loads * nt * 16;
+    fp.ring_off = moe_tab_bytes<KIND>();
+    const size_t red = (size_t)2 * 7 * 64 * TPG * 4;
+    auto kern = k_moe_front<KIND, XT, LT, TPG>;
+    const size_t fixed = static_lds(kern);
+    // direct loads land below 128 KiB; two slots where three would leave one block a CU
+    fp.nbuf = 3;
+    while (fp.nbuf > 2 && ((size_t)fp.ring_off + (size_t)fp.nbuf * fp.buf_bytes > 128 * 1024 ||
+                           fixed + fp.ring_off + (size_t)fp.nbuf * fp.buf_bytes + red > LDS_BYTES))
+      --fp.nbuf;
+    fp.red_off = fp.ring_off + fp.nbuf * fp.buf_bytes;
+    const size_t lds = (size_t)fp.red_off + red;
+    if (fp.loads > FRONT_LMAX || (size_t)fp.ring_off + (size_t)fp.nbuf * fp.buf_bytes > 128 * 1024 ||
+        lds + fixed > LDS_BYTES)
+      return fail(E_UNSUPPORTED, "moe_decode: %zu bytes of LDS for the front", lds);
+    int per_cu = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, nt, lds) != hipSuccess || per_cu < 1) per_cu = 1;
+    const int64_t most = (std::min<int64_t>(B * K, E) + 1) * (FRONT_F / 16);
+    const int64_t grid = std::min<int64_t>(most, (int64_t)device_cus() * per_cu);
+    hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(nt), lds, stream, gate, up, sg, su, logits, x, wg, (int)K,
+                       (int)B, fp, stab, ws);
     st = check_launch("moe_decode front");
+    if (st) return st;
+  }
+  if (phases & 16) {  // tail: down and the combine (the common shape)
+    const int64_t rb = row_bytes(KIND_DOWN, FRONT_F);
+    int rstride = 0, padded = 0;
+    row_layout(rb, true, rstride, padded);
+    const int64_t chunks = padded ? (int64_t)TAIL_ROWS * (rstride / 16) : (TAIL_ROWS * rb + 15) / 16 + 1;
+    const int loads = (int)((chunks + 255) / 256);
+    const size_t lds = (size_t)moe_tab_bytes<KIND_DOWN>() + (size_t)loads * 256 * 16;
+    auto kern = k_moe_tail<KIND_DOWN, XT, TPG>;
+    if (lds > 128 * 1024 || lds + static_lds(kern) > LDS_BYTES)
+      return fail(E_UNSUPPORTED, "moe_decode: %zu bytes of LDS for the tail", lds);
+    hipLaunchKernelGGL(kern, dim3((unsigned)(FRONT_D / TAIL_ROWS), (unsigned)(B * K + 1)), dim3(256), lds, stream,
+                       down, sd, (int)K, (int)B, rstride, loads, stab, ws, out);
+    st = check_launch("moe_decode tail");
     if (st) return st;
   }
   if (phases & 1) {
@@ -751,9 +991,12 @@ int moe_decode(int phases, int kind, int kind_down, const void* gate, const void
     return fail(E_WORKSPACE, "moe_decode: workspace of %zu bytes, %zu needed", workspace_bytes, need);
   MoeWs ws;
   moe_carve(&ws, (uint8_t*)workspace, tokens, k, d_model, d_ff, dtype_size(dtype));
-  // the common shape takes route, gate and up in one kernel (phase bit 8); the others the three-kernel path
-  if (experts == FRONT_E && d_model == FRONT_D) {
-    if (phases & 3) phases = (phases & ~3) | 8;
+  // the common shape takes two kernels: route, gate and up (phase bit 8), down and the combine (16); the others
+  // the three-kernel path
+  const bool aligned = ((uintptr_t)gate | (uintptr_t)up | (uintptr_t)down | (uintptr_t)shared_gate |
+                        (uintptr_t)shared_up | (uintptr_t)shared_down | (uintptr_t)x | (uintptr_t)shared_gate_w) % 16 == 0;
+  if (experts == FRONT_E && d_model == FRONT_D && d_ff == FRONT_F && aligned) {
+    phases = (phases & 3 ? 8 : 0) | (phases & 4 ? 16 : 0);
   }
   const int tpg = tokens <= 4 ? 1 : tokens <= 8 ? 2 : 4;
   if (logits_dtype != F32 && logits_dtype != dtype)
@@ -783,7 +1026,7 @@ int moe_decode(int phases, int kind, int kind_down, const void* gate, const void
     return kind == Q2_0 ? by_down(kind_c<Q2_0>{}) : by_down(kind_c<IQ3_S>{});
   });
   if (st) return st;
-  if (!(phases & 9)) return OK;
+  if (!(phases & 9)) return OK;  // the choice comes from the route or the front
   if (idx_out && hipMemcpyAsync(idx_out, ws.idx, 4 * tokens * k, hipMemcpyDeviceToDevice, (hipStream_t)stream) != hipSuccess)
     return fail(E_HIP, "moe_decode: copy of the choice failed");
   if (w_out && hipMemcpyAsync(w_out, ws.w, 4 * tokens * k, hipMemcpyDeviceToDevice, (hipStream_t)stream) != hipSuccess)

@@ -44,15 +44,40 @@ template <int KIND, int TPG, int GPER> struct XRegs {
 
 // XRegs for scale groups [gbase, gbase + GPER) of the lane's activation row xr (the row of its A-row token).
 // Q2_0: lane g's fragment a takes block-local weights k = 32h + 8g + 4a + j (j < 4, h < 2) into slot 2j + h, scaled
-// by 1 / U_j (the in-place mask's unit), as XStage stages them; IQ3_S: values 8g..8g+7 of the run as they are. The
-// sums: each lane's share, added over the four lanes of a row (xor 16, 32), then fetched from a lane whose A-row is
-// the wanted token (lane 4g + t holds token g * TPG + t).
-template <int KIND, typename XT, int TPG, int GPER>
+// by 1 / U_j (the in-place mask's unit), as XStage stages them, or as they are with RAW (for item_mac's RAW decode,
+// which shifts each code down to bit 0 instead); IQ3_S: values 8g..8g+7 of the run as they are. The sums: each
+// lane's share, added over the four lanes of a row (xor 16, 32), then fetched from a lane whose A-row is the wanted
+// token (lane 4g + t holds token g * TPG + t).
+template <int KIND, typename XT, int TPG, int GPER, bool RAW = false>
 __device__ __forceinline__ void load_x_row(XRegs<KIND, TPG, GPER>& X, const XT* xr, int gbase) {
   using MT = XT;
   const int lane = threadIdx.x & 63, g = lane >> 4;
   float part[GPER];
-  if constexpr (KIND == Q2_0) {
+  if constexpr (KIND == Q2_0 && RAW) {
+    u32x4 v[GPER][2];
+#pragma unroll
+    for (int j = 0; j < GPER; ++j) {
+      v[j][0] = *(const u32x4*)(xr + (gbase + j) * 64 + 8 * g);
+      v[j][1] = *(const u32x4*)(xr + (gbase + j) * 64 + 32 + 8 * g);
+    }
+#pragma unroll
+    for (int j = 0; j < GPER; ++j) {
+      // slot 2j + h of fragment a: x[32h + 8g + 4a + j], so each dword pairs a half of v[j][0] with the same half
+      // of v[j][1]
+      const uint32_t a0[4] = {v[j][0].x, v[j][0].y, v[j][0].z, v[j][0].w};
+      const uint32_t a1[4] = {v[j][1].x, v[j][1].y, v[j][1].z, v[j][1].w};
+      X.xa[j] = u32x4{__builtin_amdgcn_perm(a1[0], a0[0], 0x05040100u), __builtin_amdgcn_perm(a1[0], a0[0], 0x07060302u),
+                      __builtin_amdgcn_perm(a1[1], a0[1], 0x05040100u), __builtin_amdgcn_perm(a1[1], a0[1], 0x07060302u)};
+      X.xb[j] = u32x4{__builtin_amdgcn_perm(a1[2], a0[2], 0x05040100u), __builtin_amdgcn_perm(a1[2], a0[2], 0x07060302u),
+                      __builtin_amdgcn_perm(a1[3], a0[3], 0x05040100u), __builtin_amdgcn_perm(a1[3], a0[3], 0x07060302u)};
+      const XT* h0 = (const XT*)&v[j][0];
+      const XT* h1 = (const XT*)&v[j][1];
+      float p = 0.0f;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) p += to_f32(h0[i]) + to_f32(h1[i]);
+      part[j] = (Magic<MT>::BASE + 1.0f) * p;
+    }
+  } else if constexpr (KIND == Q2_0) {
     u32x4 v[GPER][2];
 #pragma unroll
     for (int j = 0; j < GPER; ++j) {
@@ -112,8 +137,9 @@ __device__ __forceinline__ void load_x(XRegs<KIND, TPG, GPER>& X, const XT* xm, 
 // one wave's item: its 16 rows (row n at wrow0 + n * rstride, already advanced to the wave's first group) x its
 // GPER groups. All LDS reads are issued up front; a group's scale is applied to its accumulator chain (two
 // chains, in turn) after the other chain's MFMAs. The D-rows past TPG are padding rows: their accumulators keep
-// whatever the chain left and are never used.
-template <int KIND, typename MT, int TPG, int GPER>
+// whatever the chain left and are never used. RAW (Q2_0): every code shifted down to bits 0-1 before its mask, for
+// activations as they are (load_x_row's RAW form).
+template <int KIND, typename MT, int TPG, int GPER, bool RAW = false>
 __device__ __forceinline__ void item_mac(const uint8_t* wrow0, int rstride, const XRegs<KIND, TPG, GPER>& X,
                                          const uint32_t* stab, const DecodeRegs& k, float* acc) {
   const int lane = threadIdx.x & 63, g = lane >> 4, n = lane & 15;
@@ -153,7 +179,20 @@ __device__ __forceinline__ void item_mac(const uint8_t* wrow0, int rstride, cons
     f32x4& Dj = D[j & 1];
 #pragma unroll
     for (int t = 0; t < TPG; ++t) Dj[t] = X.nc[j][t];
-    if constexpr (KIND == Q2_0) {
+    if constexpr (KIND == Q2_0 && RAW) {
+      const uint32_t W = w0[j] | (w1[j] << 16);
+      u32x4 fa, fb;
+      fa.x = (W & k.m0) | k.magic;
+      fa.y = ((W >> 2) & k.m0) | k.magic;
+      fa.z = ((W >> 4) & k.m0) | k.magic;
+      fa.w = ((W >> 6) & k.m0) | k.magic;
+      fb.x = ((W >> 8) & k.m0) | k.magic;
+      fb.y = ((W >> 10) & k.m0) | k.magic;
+      fb.z = ((W >> 12) & k.m0) | k.magic;
+      fb.w = ((W >> 14) & k.m0) | k.magic;
+      Dj = mfma<MT>(X.xa[j], fa, Dj);
+      Dj = mfma<MT>(X.xb[j], fb, Dj);
+    } else if constexpr (KIND == Q2_0) {
       const uint32_t W = w0[j] | (w1[j] << 16), W8 = W >> 8;
       u32x4 fa, fb;
       fa.x = (W & k.m0) | k.magic;

@@ -113,6 +113,10 @@ __device__ __forceinline__ void lds_dma16(const void* base, uint32_t off, uint32
   asm volatile("global_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base), "{m0}"(__builtin_amdgcn_readfirstlane(lds))
                : "memory");
 }
+// the same with a full address a lane (sources in different tensors within one wave's load)
+__device__ __forceinline__ void lds_dma16p(const void* src, uint32_t lds) {
+  asm volatile("global_load_lds_dwordx4 %0, off" ::"v"(src), "{m0}"(__builtin_amdgcn_readfirstlane(lds)) : "memory");
+}
 // the LDS byte address of a __shared__ array (cast on the array itself: no null check of a generic pointer)
 #define SH_LDS_ADDR(arr) ((uint32_t)(uintptr_t)(__attribute__((address_space(3))) void*)(arr))
 
