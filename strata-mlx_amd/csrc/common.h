@@ -27,6 +27,19 @@ __host__ __device__ constexpr int bpb(int k) {
 
 __host__ __device__ constexpr int64_t row_bytes_dev(int k, int64_t cols) { return cols / wpb(k) * bpb(k); }
 
+// the LDS stride of rows of rbytes (a multiple of 16): padded by 16-byte chunks so 16 consecutive rows start in
+// distinct 4-bank windows of the 64 banks
+__host__ __device__ constexpr int padded_stride(int rbytes) {
+  for (int pad = 0; pad <= 48; pad += 16) {
+    const int dw = (rbytes + pad) / 4;
+    bool distinct = true;
+    for (int a = 0; a < 16 && distinct; ++a)
+      for (int b = a + 1; b < 16 && distinct; ++b) distinct = ((a * dw) % 64) / 4 != ((b * dw) % 64) / 4;
+    if (distinct) return rbytes + pad;
+  }
+  return rbytes + 16;
+}
+
 // Codebook blob: every table one kernel may need, at fixed 16-byte aligned offsets. The blob is device memory
 // the caller uploads once; kernels that need a table copy it to LDS.
 constexpr int TAB_KVALUES = 0;       // int8 [16]        IQ4_NL / IQ4_XS values (strata_mlx/gguf.py:34)

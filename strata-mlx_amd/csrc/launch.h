@@ -95,18 +95,7 @@ inline void row_layout(int64_t rbytes, bool aligned, int& rstride, int& padded) 
   padded = 0;
   rstride = (int)rbytes;
   if (rbytes % 16 || !aligned) return;
-  for (int pad = 0; pad <= 48; pad += 16) {
-    const int dw = (int)(rbytes + pad) / 4;
-    bool distinct = true;
-    for (int a = 0; a < 16 && distinct; ++a)
-      for (int b = a + 1; b < 16 && distinct; ++b) distinct = ((a * dw) % 64) / 4 != ((b * dw) % 64) / 4;
-    if (distinct) {
-      rstride = (int)rbytes + pad;
-      padded = 1;
-      return;
-    }
-  }
-  rstride = (int)rbytes + 16;
+  rstride = padded_stride((int)rbytes);
   padded = 1;
 }
 

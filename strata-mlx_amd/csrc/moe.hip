@@ -307,21 +307,30 @@ __global__ __launch_bounds__(256) void k_moe_gate_up(const uint8_t* __restrict__
 //        the activation type and writes swiglu(gate, up) per pair, in natural order. Block 0 also writes the
 //        choice, its weights and the group table and clears the tail's counters; block 1 the shared expert's gate
 //        logits.
-// tail   down and the combine. Block (tile, g) multiplies 64 rows of down of group g's expert (a wave 16 rows,
-//        all 512 columns) and writes each pair's outputs, rounded to the activation type, to the workspace; the
-//        last block of a row tile to finish (a counter per tile) combines the tile for every token.
+// tail   down and the combine. Its blocks stream contiguous runs of the items (group g, row tile of 128 rows of
+//        down of g's expert; a wave 16 rows, all 512 columns) through an LDS ring as the front does, writing each
+//        pair's outputs, rounded to the activation type, to the workspace; the block that completes a row tile's
+//        count of items combines the tile for every token.
 
 constexpr int FRONT_E = 512, FRONT_D = 2048, FRONT_F = 512;
-constexpr int FRONT_WAVES = 8, FRONT_LMAX = 6;
-constexpr int TAIL_ROWS = 64;  // rows of down a tail block
+constexpr int FRONT_WAVES = 8;
+
+// an item in LDS: 16 rows of gate then 16 of up at a padded stride, as 16-byte chunks; wave w loads the runs of 64
+// chunks w, w + 8, ... (the last run's chunks past the item re-read its last chunk into the slot's tail)
+template <int KIND> struct FrontItem {
+  static constexpr int RB = (int)row_bytes_dev(KIND, FRONT_D);
+  static constexpr int RSTRIDE = padded_stride(RB);
+  static constexpr int CPR = RSTRIDE / 16, CPR_SRC = RB / 16;
+  static constexpr int CHUNKS = 2 * 16 * CPR, RUNS = (CHUNKS + 63) / 64;
+  static constexpr int SLOT = RUNS * 1024;
+  static constexpr int LOADS = (RUNS + FRONT_WAVES - 1) / FRONT_WAVES;  // of the waves with the most
+  static_assert(RB % 16 == 0 && RUNS >= FRONT_WAVES, "front item layout");
+};
 
 struct FrontPlan {
-  int rstride;    // LDS bytes a row (padded so a wave's 16 rows fall in distinct banks)
-  int loads;      // direct loads a thread an item
-  int nbuf;       // ring slots
-  int buf_bytes;  // bytes a slot
-  int ring_off;   // after the IQ3_S table
-  int red_off;    // [2][7][64][TPG] floats: gate's and up's partial sums of waves 1..7
+  int nbuf;      // ring slots
+  int ring_off;  // after the IQ3_S table
+  int red_off;   // [2][7][64][TPG] floats: gate's and up's partial sums of waves 1..7
 };
 
 template <int KIND, typename XT, typename LT, int TPG>
@@ -335,8 +344,8 @@ __global__ __launch_bounds__(FRONT_WAVES * 64) void k_moe_front(
   constexpr int E = FRONT_E, D = FRONT_D, F = FRONT_F, VPL = E / 64, WORDS = E / 32, TILES = F / 16;
   constexpr int NT = FRONT_WAVES * 64;
   constexpr int GPER = KIND == Q2_0 ? D / 64 / FRONT_WAVES : D / 32 / FRONT_WAVES;  // a wave's eighth of the groups
-  constexpr int RB = (int)row_bytes_dev(KIND, D);
-  constexpr int CPR_SRC = RB / 16;
+  using IT = FrontItem<KIND>;
+  constexpr int RB = IT::RB;
   extern __shared__ u32x4 dyn[];
   uint8_t* lds = (uint8_t*)dyn;
   const uint32_t lds_base = SH_LDS_ADDR(dyn);
@@ -430,7 +439,7 @@ __global__ __launch_bounds__(FRONT_WAVES * 64) void k_moe_front(
       ws.w[tid] = s_wt[tid];
     }
     if (tid < groups) ws.g_expert[tid] = s_gexp[tid];
-    if (tid < D / TAIL_ROWS) ws.cnt[tid] = 0;
+    if (tid < D / 64) ws.cnt[tid] = 0;  // the tail's row tiles
     if (tid == 0) *ws.n_groups = groups;
   }
   if (blockIdx.x == 1 % gridDim.x) {  // the shared expert's gate logit of each token, rounded to the activation type
@@ -457,17 +466,17 @@ __global__ __launch_bounds__(FRONT_WAVES * 64) void k_moe_front(
   if (first >= last) return;  // block-uniform
 
   // this thread's chunks of an item: matrix (0 gate, 1 up) and byte offset from the item's first row; the slot's
-  // tail past the two matrices re-reads up's last chunk
-  const int cpr = fp.rstride >> 4;
-  int pre_off[FRONT_LMAX];
-  bool pre_up[FRONT_LMAX];
+  // tail past the two matrices re-reads up's last chunk. Each wave waits on its own count of loads.
+  const int loads = (IT::RUNS - wave + FRONT_WAVES - 1) / FRONT_WAVES;
+  int pre_off[IT::LOADS];
+  bool pre_up[IT::LOADS];
 #pragma unroll
-  for (int j = 0; j < FRONT_LMAX; ++j) {
+  for (int j = 0; j < IT::LOADS; ++j) {
     const int s = (j * FRONT_WAVES + wave) * 64 + lane;
-    const int m = s / (16 * cpr), rem = s - m * 16 * cpr;
-    const int row = rem / cpr, kk = rem - row * cpr;
+    const int m = s / (16 * IT::CPR), rem = s - m * 16 * IT::CPR;
+    const int row = rem / IT::CPR, kk = rem - row * IT::CPR;
     pre_up[j] = m >= 1;
-    pre_off[j] = m >= 2 ? 15 * RB + 16 * (CPR_SRC - 1) : row * RB + 16 * min(kk, CPR_SRC - 1);
+    pre_off[j] = m >= 2 ? 15 * RB + 16 * (IT::CPR_SRC - 1) : row * RB + 16 * min(kk, IT::CPR_SRC - 1);
   }
   const int64_t ebytes = (int64_t)F * RB;
   auto issue = [&](int item) {
@@ -475,10 +484,10 @@ __global__ __launch_bounds__(FRONT_WAVES * 64) void k_moe_front(
     const int e = s_gexp[g];
     const uint8_t* gs = (e == E ? sh_gate : gate + (int64_t)e * ebytes) + (int64_t)r * 16 * RB;
     const uint8_t* us = (e == E ? sh_up : up + (int64_t)e * ebytes) + (int64_t)r * 16 * RB;
-    const uint32_t buf = lds_base + fp.ring_off + (item % fp.nbuf) * fp.buf_bytes + wave * 1024;
+    const uint32_t buf = lds_base + fp.ring_off + (item % fp.nbuf) * IT::SLOT + wave * 1024;
 #pragma unroll
-    for (int j = 0; j < FRONT_LMAX; ++j)
-      if (j < fp.loads) lds_dma16p((pre_up[j] ? us : gs) + pre_off[j], buf + j * (NT * 16));
+    for (int j = 0; j < IT::LOADS; ++j)
+      if (j < loads) lds_dma16p((pre_up[j] ? us : gs) + pre_off[j], buf + j * (NT * 16));
   };
   for (int k = 0; k < fp.nbuf - 1 && first + k < last; ++k) issue(first + k);
 
@@ -499,7 +508,7 @@ __global__ __launch_bounds__(FRONT_WAVES * 64) void k_moe_front(
   int g_cur = -1, n_tok = 0;
   for (int item = first; item < last; ++item) {
     const int ahead = min(fp.nbuf - 2, last - 1 - item);  // items issued after this one
-    wait_vmcnt(ahead * fp.loads);
+    wait_vmcnt(ahead * loads);
     lds_sync();  // this item is in LDS for every wave; every wave is done with the item before
     store_h();
     if (item + fp.nbuf - 1 < last) issue(item + fp.nbuf - 1);
@@ -528,10 +537,10 @@ __global__ __launch_bounds__(FRONT_WAVES * 64) void k_moe_front(
     float acc_g[TPG], acc_u[TPG];
 #pragma unroll
     for (int t = 0; t < TPG; ++t) acc_g[t] = acc_u[t] = 0.0f;
-    const uint8_t* row0 = lds + fp.ring_off + (item % fp.nbuf) * fp.buf_bytes + wcol;
+    const uint8_t* row0 = lds + fp.ring_off + (item % fp.nbuf) * IT::SLOT + wcol;
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-    item_mac<KIND, MT, TPG, GPER, true>(row0, fp.rstride, X, (const uint32_t*)lds, kr, acc_g);
-    item_mac<KIND, MT, TPG, GPER, true>(row0 + 16 * fp.rstride, fp.rstride, X, (const uint32_t*)lds, kr, acc_u);
+    item_mac<KIND, MT, TPG, GPER, true>(row0, IT::RSTRIDE, X, (const uint32_t*)lds, kr, acc_g);
+    item_mac<KIND, MT, TPG, GPER, true>(row0 + 16 * IT::RSTRIDE, IT::RSTRIDE, X, (const uint32_t*)lds, kr, acc_u);
     if (wave > 0) {
 #pragma unroll
       for (int t = 0; t < TPG; ++t) {
@@ -561,144 +570,198 @@ __global__ __launch_bounds__(FRONT_WAVES * 64) void k_moe_front(
   store_h();
 }
 
+// an item of the tail: 64 rows of down (wave (r, h): rows 16r.. of column half h), 16-byte chunks copied as they
+// lie (the rows of a Q2_0 / IQ3_S expert of width 512 are 144 / 220 bytes: 16 rows at that stride fall in distinct
+// or two-way shared bank windows); wave w loads the runs of 64 chunks w, w + 8, ...
+template <int KIND> struct TailItem {
+  static constexpr int RB = (int)row_bytes_dev(KIND, FRONT_F);
+  static constexpr int ROWS = 64, TILES = FRONT_D / ROWS;
+  static constexpr int CHUNKS = ROWS * RB / 16, RUNS = (CHUNKS + 63) / 64;
+  static constexpr int SLOT = RUNS * 1024;
+  static constexpr int LOADS = (RUNS + FRONT_WAVES - 1) / FRONT_WAVES;
+  static_assert(ROWS * RB % 16 == 0 && RUNS >= FRONT_WAVES && FRONT_WAVES == 8, "tail item layout");
+};
+
+struct TailPlan {
+  int nbuf;      // ring slots
+  int ring_off;  // after the IQ3_S table
+  int red_off;   // [4][64][TPG] floats: the second column half's sums
+};
+
 template <int KIND, typename XT, int TPG>
-__global__ __launch_bounds__(256) void k_moe_tail(const uint8_t* __restrict__ down, const uint8_t* __restrict__ sh_down,
-                                                  int K, int B, int rstride, int loads,
-                                                  const uint8_t* __restrict__ signed_tab, MoeWs ws,
-                                                  XT* __restrict__ out) {
+__global__ __launch_bounds__(FRONT_WAVES * 64) void k_moe_tail(const uint8_t* __restrict__ down,
+                                                               const uint8_t* __restrict__ sh_down, int K, int B,
+                                                               TailPlan tp, const uint8_t* __restrict__ signed_tab,
+                                                               MoeWs ws, XT* __restrict__ out) {
 #pragma clang fp contract(off)
   using MT = XT;
-  constexpr int E = FRONT_E, D = FRONT_D, F = FRONT_F;
-  constexpr int GPER = KIND == Q2_0 ? F / 64 : F / 32;  // a wave's 16 rows whole
-  constexpr int RB = (int)row_bytes_dev(KIND, F);
+  using IT = TailItem<KIND>;
+  constexpr int E = FRONT_E, D = FRONT_D, F = FRONT_F, NT = FRONT_WAVES * 64, TILES = IT::TILES;
+  constexpr int GPER = KIND == Q2_0 ? F / 64 / 2 : F / 32 / 2;  // a wave's half of the columns
+  constexpr int RB = IT::RB;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int tile = blockIdx.x, gy = blockIdx.y;
+  const int rg = wave & 3, kh = wave >> 2;
+  const int wcol = KIND == Q2_0 ? kh * GPER * 18 : kh * 110;
   const int P = B * K;
-  __shared__ int s_groups, s_e, s_last;
-  __shared__ int s_idx[MOE_MAX_PAIRS];
-  __shared__ int s_wp[4][16];
+  __shared__ int s_groups, s_ncomb;
+  __shared__ int s_idx[MOE_MAX_PAIRS], s_gexp[MOE_MAX_PAIRS + 1], s_comb[MOE_MAX_PAIRS + 1];
+  __shared__ int s_wp[FRONT_WAVES][16];
   extern __shared__ u32x4 dyn[];
   uint8_t* lds = (uint8_t*)dyn;
   const uint32_t lds_base = SH_LDS_ADDR(dyn);
+  float* red = (float*)(lds + tp.red_off);
 
-  if (tid == 0) s_groups = *ws.n_groups;
-  if (tid == 1) s_e = ws.g_expert[gy];
-  if (tid < P) s_idx[tid] = ws.idx[tid];
-  __syncthreads();
-  if (gy >= s_groups) return;  // block-uniform: past the groups the front found
-  const int e = s_e;
-  // the rows: direct loads into LDS, 16-byte chunks of the 64 rows (rstride == RB: packed from the chunk holding
-  // the first byte; padded: rows at rstride, each row's chunks re-reading its last past its end)
-  const int ring_off = KIND == IQ3_S ? IQ3S_SIGNED_BYTES : 0;
-  const uint8_t* src = (e == E ? sh_down : down + (int64_t)e * D * RB) + (int64_t)tile * TAIL_ROWS * RB;
-  {
-    const bool padded = rstride != RB;
-    const int cpr = rstride >> 4;
-    const int nb = TAIL_ROWS * RB;
-    const uint8_t* base = padded ? src : (const uint8_t*)((uintptr_t)src & ~(uintptr_t)15);
-    const int lastc = padded ? nb - 16 : ((lead_of(src) + nb - 1) & ~15);
-    for (int j = 0; j < loads; ++j) {  // loads is the same for every wave: each issues exactly `loads`
-      const int s = (j * 4 + wave) * 64 + lane;
-      int off;
-      if (padded) {
-        const int row = s / cpr, kk = s - row * cpr;
-        off = row * RB + 16 * min(kk, RB / 16 - 1);
-      } else {
-        off = 16 * s;
-      }
-      lds_dma16(base, min(off, lastc), lds_base + ring_off + (j * 4 + wave) * 1024);
-    }
-  }
+  // the IQ3_S table (it waits on nothing), then the front's choice and groups in one trip
   if constexpr (KIND == IQ3_S) {
 #pragma unroll
-    for (int i = 0; i < IQ3S_SIGNED_BYTES / 16 / 256; ++i) {
-      const int c0 = wave * 64 + i * 256;
+    for (int i = 0; i < IQ3S_SIGNED_BYTES / 16 / NT; ++i) {
+      const int c0 = wave * 64 + i * NT;
       lds_dma16(signed_tab, 16 * (c0 + lane), lds_base + 16 * c0);
     }
   }
-  // the group's tokens (each wave for itself) and their fragments of h
-  int n_tok;
-  if (e < E) {
-    int jh = -1;
-    if (lane < B)
-      for (int j = 0; j < K; ++j)
-        if (s_idx[lane * K + j] == e) jh = j;
-    const uint64_t bal = __ballot(jh >= 0);
-    n_tok = __popcll(bal);
-    if (jh >= 0) s_wp[wave][__popcll(bal & ((1ull << lane) - 1ull))] = lane * K + jh;
-  } else {
-    n_tok = B;
-    if (lane < B) s_wp[wave][lane] = P + lane;
+  if (tid == 0) {
+    s_groups = *ws.n_groups;
+    s_ncomb = 0;
   }
-  __builtin_amdgcn_wave_barrier();
-  int mt = lane_token<TPG>();
-  mt = mt < n_tok ? mt : 0;
-  XRegs<KIND, TPG, GPER> X;
-  load_x_row<KIND, XT, TPG, GPER, true>(X, (const XT*)ws.h + (int64_t)s_wp[wave][mt] * F, 0);
+  if (tid < P) s_idx[tid] = ws.idx[tid];
+  if (tid <= P) s_gexp[tid] = ws.g_expert[tid];  // entries past the groups are never read
+  __syncthreads();
+  const int groups = s_groups;
+  const int items = groups * TILES;
+  const int per = (items + gridDim.x - 1) / gridDim.x;
+  const int first = blockIdx.x * per, last = min(items, first + per);
+  if (first >= last) return;  // block-uniform; the barrier above waited for the table
+
+  const int loads = (IT::RUNS - wave + FRONT_WAVES - 1) / FRONT_WAVES;
+  int pre_off[IT::LOADS];
+#pragma unroll
+  for (int j = 0; j < IT::LOADS; ++j) pre_off[j] = 16 * min((j * FRONT_WAVES + wave) * 64 + lane, IT::CHUNKS - 1);
+  auto issue = [&](int item) {
+    const int g = item / TILES, tile = item - g * TILES;
+    const int e = __builtin_amdgcn_readfirstlane(s_gexp[g]);  // block-uniform: a scalar base
+    const uint8_t* src = (e == E ? sh_down : down + (int64_t)e * D * RB) + (int64_t)tile * IT::ROWS * RB;
+    const uint32_t buf = lds_base + tp.ring_off + (item % tp.nbuf) * IT::SLOT + wave * 1024;
+#pragma unroll
+    for (int j = 0; j < IT::LOADS; ++j)
+      if (j < loads) lds_dma16(src, pre_off[j], buf + j * (NT * 16));
+  };
+  for (int k = 0; k < tp.nbuf - 1 && first + k < last; ++k) issue(first + k);
+
   const DecodeRegs kr = decode_regs<KIND, MT>();
-  wait_vmcnt(0);
-  lds_sync();
-  float acc[TPG];
+  XRegs<KIND, TPG, GPER> X;
+  // each pair's outputs, rounded to the activation type, go out as device-scope stores (through the XCD's L2 to
+  // memory) at the start of the next item
+  float yv[TPG];
+  int yp[TPG], yrow = -1;
+  auto store_y = [&]() {
+    if (yrow >= 0) {
 #pragma unroll
-  for (int t = 0; t < TPG; ++t) acc[t] = 0.0f;
-  const uint8_t* row0 = lds + ring_off + (rstride != RB ? 0 : lead_of(src)) + wave * 16 * rstride;
-  item_mac<KIND, MT, TPG, GPER, true>(row0, rstride, X, (const uint32_t*)lds, kr, acc);
-  // each pair's 16 outputs of this wave, rounded to the activation type
-  {
-    const int q = lane >> 4, n = lane & 15;
-    const int row = tile * TAIL_ROWS + wave * 16 + n;
-#pragma unroll
-    for (int t = 0; t < TPG; ++t) {
-      const int tt = q * TPG + t;
-      if (tt < n_tok)
-        __hip_atomic_store(&ws.y[(int64_t)s_wp[wave][tt] * D + row], to_f32(from_f32<XT>(acc[t])), __ATOMIC_RELAXED,
-                           __HIP_MEMORY_SCOPE_AGENT);
+      for (int t = 0; t < TPG; ++t)
+        if (yp[t] >= 0)
+          __hip_atomic_store(&ws.y[(int64_t)yp[t] * D + yrow], yv[t], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
-  }
-  // The last block of the tile to count itself combines it. The outputs go out as device-scope stores (written
-  // through the XCD's L2) and are complete (vmcnt 0) before the count; the combining block reads them with
-  // device-scope loads after it. No device-wide fence: its L2 write-back and invalidation serialize the tile's
-  // blocks on each XCD's L2.
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  __syncthreads();
-  if (tid == 0)
-    s_last = __hip_atomic_fetch_add(&ws.cnt[tile], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == s_groups - 1;
-  __syncthreads();
-  if (!s_last) return;
-  // the combine (strata_mlx/fused.py:448-462): experts in 8 rows j taking k = j, j + 8, ..., each product rounded
-  for (int qv = tid; qv < B * TAIL_ROWS; qv += 256) {
-    const int t = qv / TAIL_ROWS, row = tile * TAIL_ROWS + qv % TAIL_ROWS;
-    float yv[16], wv[16];  // k <= 16
-#pragma unroll
-    for (int kk = 0; kk < 16; ++kk) {
-      yv[kk] = kk < K ? __hip_atomic_load(&ws.y[(int64_t)(t * K + kk) * D + row], __ATOMIC_RELAXED,
-                                          __HIP_MEMORY_SCOPE_AGENT) : 0.0f;
-      wv[kk] = kk < K ? ws.w[t * K + kk] : 0.0f;
+  };
+  int g_cur = -1, n_tok = 0;
+  for (int item = first; item < last; ++item) {
+    const int ahead = min(tp.nbuf - 2, last - 1 - item);
+    wait_vmcnt(ahead * loads);
+    lds_sync();
+    store_y();
+    if (item + tp.nbuf - 1 < last) issue(item + tp.nbuf - 1);
+    const int g = item / TILES, tile = item - g * TILES;
+    if (g != g_cur) {  // a new group: its tokens in token order (each wave for itself), their fragments of h
+      g_cur = g;
+      const int e = s_gexp[g];
+      if (e < E) {
+        int jh = -1;
+        if (lane < B)
+          for (int j = 0; j < K; ++j)
+            if (s_idx[lane * K + j] == e) jh = j;
+        const uint64_t bal = __ballot(jh >= 0);
+        n_tok = __popcll(bal);
+        if (jh >= 0) s_wp[wave][__popcll(bal & ((1ull << lane) - 1ull))] = lane * K + jh;
+      } else {
+        n_tok = B;
+        if (lane < B) s_wp[wave][lane] = P + lane;
+      }
+      __builtin_amdgcn_wave_barrier();
+      int mt = lane_token<TPG>();
+      mt = mt < n_tok ? mt : 0;
+      load_x_row<KIND, XT, TPG, GPER, true>(X, (const XT*)ws.h + (int64_t)s_wp[wave][mt] * F, kh * GPER);
     }
-    const float ys = __hip_atomic_load(&ws.y[(int64_t)(P + t) * D + row], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    float acc2 = 0.0f;
+    float acc[TPG];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      if (j < K) {
-        float part = 0.0f;
+    for (int t = 0; t < TPG; ++t) acc[t] = 0.0f;
+    const uint8_t* row0 = lds + tp.ring_off + (item % tp.nbuf) * IT::SLOT + rg * 16 * RB + wcol;
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    item_mac<KIND, MT, TPG, GPER, true>(row0, RB, X, (const uint32_t*)lds, kr, acc);
+    if (kh == 1) {
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
-          const int kk = j + 8 * i;
-          if (kk < K) {
-            const float prod = yv[kk] * wv[kk];
-            part = prod + part;
-          }
-        }
-        acc2 = j == 0 ? part : part + acc2;
+      for (int t = 0; t < TPG; ++t) red[(rg * 64 + lane) * TPG + t] = acc[t];
+    }
+    lds_sync();
+    if (kh == 0) {
+      const int q = lane >> 4, n = lane & 15;
+      yrow = tile * IT::ROWS + rg * 16 + n;
+#pragma unroll
+      for (int t = 0; t < TPG; ++t) {
+        const int tt = q * TPG + t;
+        yv[t] = to_f32(from_f32<XT>(acc[t] + red[(rg * 64 + lane) * TPG + t]));
+        yp[t] = tt < n_tok ? s_wp[wave][tt] : -1;
       }
     }
-    const XT routed = from_f32<XT>(acc2);
-    const XT gate = from_f32<XT>(1.0f / (1.0f + expf(-ws.gsh[t])));
-    const XT shared = from_f32<XT>(to_f32(gate) * ys);
-    out[(int64_t)t * D + row] = from_f32<XT>(to_f32(routed) + to_f32(shared));
   }
-  if (tid == 0) __hip_atomic_store(&ws.cnt[tile], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  store_y();
+  // Count this block's items into their row tiles' counters once every output of them is out (vmcnt 0: the
+  // device-scope stores reached memory); the block that completes a tile's count combines the tile, reading the
+  // outputs with device-scope loads. No device-wide fence: its L2 write-back and invalidation serialize the
+  // blocks of an XCD.
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  if (tid < last - first) {
+    const int tile = (first + tid) % TILES;
+    if (__hip_atomic_fetch_add(&ws.cnt[tile], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == groups - 1)
+      s_comb[atomicAdd(&s_ncomb, 1)] = tile;
+  }
+  __syncthreads();
+  const int ncomb = s_ncomb;
+  // the combine (strata_mlx/fused.py:448-462): experts in 8 rows j taking k = j, j + 8, ..., each product rounded
+  for (int c = 0; c < ncomb; ++c) {
+    const int tile = s_comb[c];
+    for (int qv = tid; qv < B * IT::ROWS; qv += NT) {
+      const int t = qv / IT::ROWS, row = tile * IT::ROWS + qv % IT::ROWS;
+      float y[16], w[16];  // k <= 16
+#pragma unroll
+      for (int kk = 0; kk < 16; ++kk) {
+        y[kk] = kk < K ? __hip_atomic_load(&ws.y[(int64_t)(t * K + kk) * D + row], __ATOMIC_RELAXED,
+                                           __HIP_MEMORY_SCOPE_AGENT) : 0.0f;
+        w[kk] = kk < K ? ws.w[t * K + kk] : 0.0f;
+      }
+      const float ys = __hip_atomic_load(&ws.y[(int64_t)(P + t) * D + row], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      float acc2 = 0.0f;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        if (j < K) {
+          float part = 0.0f;
+#pragma unroll
+          for (int i = 0; i < 2; ++i) {
+            const int kk = j + 8 * i;
+            if (kk < K) {
+              const float prod = y[kk] * w[kk];
+              part = prod + part;
+            }
+          }
+          acc2 = j == 0 ? part : part + acc2;
+        }
+      }
+      const XT routed = from_f32<XT>(acc2);
+      const XT gate = from_f32<XT>(1.0f / (1.0f + expf(-ws.gsh[t])));
+      const XT shared = from_f32<XT>(to_f32(gate) * ys);
+      out[(int64_t)t * D + row] = from_f32<XT>(to_f32(routed) + to_f32(shared));
+    }
+    if (tid == 0) __hip_atomic_store(&ws.cnt[tile], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
 }
 
 // ---- down and the combine: a block is 16 output rows of every group's expert
@@ -878,26 +941,21 @@ static int launch_moe(const uint8_t* gate, const uint8_t* up, const uint8_t* dow
   const uint8_t* stab = tables ? tables + TAB_IQ3S_SIGNED : nullptr;
   int st = OK;
   if (phases & 8) {  // front: route, gate and up (the common shape)
+    using IT = FrontItem<KIND>;
     FrontPlan fp;
-    const int64_t rb = row_bytes(KIND, FRONT_D);
-    int padded = 0;
-    row_layout(rb, true, fp.rstride, padded);
     const int nt = FRONT_WAVES * 64;
-    fp.loads = (int)((2 * 16 * (fp.rstride / 16) + nt - 1) / nt);
-    fp.buf_bytes = fp.loads * nt * 16;
     fp.ring_off = moe_tab_bytes<KIND>();
     const size_t red = (size_t)2 * 7 * 64 * TPG * 4;
     auto kern = k_moe_front<KIND, XT, LT, TPG>;
     const size_t fixed = static_lds(kern);
-    // direct loads land below 128 KiB; two slots where three would leave one block a CU
+    // direct loads land below 128 KiB
     fp.nbuf = 3;
-    while (fp.nbuf > 2 && ((size_t)fp.ring_off + (size_t)fp.nbuf * fp.buf_bytes > 128 * 1024 ||
-                           fixed + fp.ring_off + (size_t)fp.nbuf * fp.buf_bytes + red > LDS_BYTES))
+    while (fp.nbuf > 2 && ((size_t)fp.ring_off + (size_t)fp.nbuf * IT::SLOT > 128 * 1024 ||
+                           fixed + fp.ring_off + (size_t)fp.nbuf * IT::SLOT + red > LDS_BYTES))
       --fp.nbuf;
-    fp.red_off = fp.ring_off + fp.nbuf * fp.buf_bytes;
+    fp.red_off = fp.ring_off + fp.nbuf * IT::SLOT;
     const size_t lds = (size_t)fp.red_off + red;
-    if (fp.loads > FRONT_LMAX || (size_t)fp.ring_off + (size_t)fp.nbuf * fp.buf_bytes > 128 * 1024 ||
-        lds + fixed > LDS_BYTES)
+    if ((size_t)fp.ring_off + (size_t)fp.nbuf * IT::SLOT > 128 * 1024 || lds + fixed > LDS_BYTES)
       return fail(E_UNSUPPORTED, "moe_decode: %zu bytes of LDS for the front", lds);
     int per_cu = 0;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, nt, lds) != hipSuccess || per_cu < 1) per_cu = 1;
@@ -909,17 +967,28 @@ static int launch_moe(const uint8_t* gate, const uint8_t* up, const uint8_t* dow
     if (st) return st;
   }
   if (phases & 16) {  // tail: down and the combine (the common shape)
-    const int64_t rb = row_bytes(KIND_DOWN, FRONT_F);
-    int rstride = 0, padded = 0;
-    row_layout(rb, true, rstride, padded);
-    const int64_t chunks = padded ? (int64_t)TAIL_ROWS * (rstride / 16) : (TAIL_ROWS * rb + 15) / 16 + 1;
-    const int loads = (int)((chunks + 255) / 256);
-    const size_t lds = (size_t)moe_tab_bytes<KIND_DOWN>() + (size_t)loads * 256 * 16;
+    using IT = TailItem<KIND_DOWN>;
+    TailPlan tp;
+    tp.ring_off = moe_tab_bytes<KIND_DOWN>();
     auto kern = k_moe_tail<KIND_DOWN, XT, TPG>;
-    if (lds > 128 * 1024 || lds + static_lds(kern) > LDS_BYTES)
+    const size_t fixed = static_lds(kern);
+    const size_t red = (size_t)4 * 64 * TPG * 4;
+    tp.nbuf = 4;
+    while (tp.nbuf > 2 && ((size_t)tp.ring_off + (size_t)tp.nbuf * IT::SLOT > 128 * 1024 ||
+                           fixed + tp.ring_off + (size_t)tp.nbuf * IT::SLOT + red > LDS_BYTES))
+      --tp.nbuf;
+    tp.red_off = tp.ring_off + tp.nbuf * IT::SLOT;
+    const size_t lds = (size_t)tp.red_off + red;
+    if ((size_t)tp.red_off > 128 * 1024 || lds + fixed > LDS_BYTES)
       return fail(E_UNSUPPORTED, "moe_decode: %zu bytes of LDS for the tail", lds);
-    hipLaunchKernelGGL(kern, dim3((unsigned)(FRONT_D / TAIL_ROWS), (unsigned)(B * K + 1)), dim3(256), lds, stream,
-                       down, sd, (int)K, (int)B, rstride, loads, stab, ws, out);
+    const int nt = FRONT_WAVES * 64;
+    int per_cu = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, nt, lds) != hipSuccess || per_cu < 1) per_cu = 1;
+    const int64_t most = (std::min<int64_t>(B * K, E) + 1) * IT::TILES;
+    const int64_t grid = std::min<int64_t>(most, (int64_t)device_cus() * per_cu);
+    if ((most + grid - 1) / grid > MOE_MAX_PAIRS)  // a block's items, each counted by a thread of its own
+      return fail(E_UNSUPPORTED, "moe_decode: %lld tail items a block", (long long)((most + grid - 1) / grid));
+    hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(nt), lds, stream, down, sd, (int)K, (int)B, tp, stab, ws, out);
     st = check_launch("moe_decode tail");
     if (st) return st;
   }
