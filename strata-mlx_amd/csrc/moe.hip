@@ -106,6 +106,52 @@ template <> struct RouteKey<float> {
   __device__ static __forceinline__ uint64_t wave_max(uint64_t k) { return wave_max_u64(k); }
 };
 
+// One token's top-k by selection instead of k rounds of arg-max: the k-th largest key found bit by bit from the top
+// (a candidate stays if at least k keys are at or above it: eight ballots and popcounts a bit), over the value bits
+// first and over the index bits only when the k-th value is tied past k; then the k keys at or above it, ranked
+// among themselves. Lane l holds keys i * 64 + l (i < VPL), unique, the larger chosen first (RouteKey). Leaves
+// the chosen keys in descending order in sorted[0, k) (LDS, the wave's own; scratch the same size).
+template <typename RK, int VPL>
+__device__ __forceinline__ void wave_top_k(const typename RK::type (&key)[VPL], int K, typename RK::type* scratch,
+                                           typename RK::type* sorted) {
+  using key_t = typename RK::type;
+  constexpr int BITS = 8 * (int)sizeof(key_t), IBITS = BITS / 2;  // the low half holds the index
+  const int lane = threadIdx.x & 63;
+  auto count_ge = [&](key_t c) {
+    int n = 0;
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) n += __popcll(__ballot(key[i] >= c));
+    return n;
+  };
+  key_t prefix = 0;
+  for (int bit = BITS - 1; bit >= IBITS; --bit) {
+    const key_t cand = prefix | ((key_t)1 << bit);
+    if (count_ge(cand) >= K) prefix = cand;
+  }
+  if (count_ge(prefix) != K) {  // the k-th value is tied past k: the lower indices first
+    for (int bit = IBITS - 1; bit >= 0; --bit) {
+      const key_t cand = prefix | ((key_t)1 << bit);
+      if (count_ge(cand) >= K) prefix = cand;
+    }
+  }
+  int base = 0;
+#pragma unroll
+  for (int i = 0; i < VPL; ++i) {
+    const bool sel = key[i] >= prefix;
+    const uint64_t m = __ballot(sel);
+    if (sel) scratch[base + __popcll(m & ((1ull << lane) - 1ull))] = key[i];
+    base += __popcll(m);
+  }
+  __builtin_amdgcn_wave_barrier();
+  if (lane < K) {
+    const key_t mine = scratch[lane];
+    int rank = 0;
+    for (int j = 0; j < K; ++j) rank += scratch[j] > mine;
+    sorted[rank] = mine;
+  }
+  __builtin_amdgcn_wave_barrier();
+}
+
 template <int KIND, typename XT, typename LT, int VPL>
 __global__ __launch_bounds__(256) void k_moe_route(const LT* __restrict__ logits, const XT* __restrict__ x,
                                                    const XT* __restrict__ wg, int B, int E, int K, int D, MoeWs ws) {
@@ -315,6 +361,40 @@ __global__ __launch_bounds__(256) void k_moe_gate_up(const uint8_t* __restrict__
 constexpr int FRONT_E = 512, FRONT_D = 2048, FRONT_F = 512;
 constexpr int FRONT_WAVES = 8;
 
+// the pairs of group expert e in token order, into this wave's wp[0, n): pair t * K + j of each token t choosing e
+// (a token chooses an expert at most once), or every token's shared pair P + t for the shared expert (e == E)
+__device__ __forceinline__ int group_pairs(int e, int E, const int* s_idx, int B, int K, int* wp) {
+  const int lane = threadIdx.x & 63;
+  int n;
+  if (e < E) {
+    int jh = -1;
+    if (lane < B)
+      for (int j = 0; j < K; ++j)
+        if (s_idx[lane * K + j] == e) jh = j;
+    const uint64_t bal = __ballot(jh >= 0);
+    n = __popcll(bal);
+    if (jh >= 0) wp[__popcll(bal & ((1ull << lane) - 1ull))] = lane * K + jh;
+  } else {
+    n = B;
+    if (lane < B) wp[lane] = B * K + lane;
+  }
+  __builtin_amdgcn_wave_barrier();
+  return n;
+}
+
+// a block's run of items: chunk c of group g's TILES items, chunks of `per` items, per the least that leaves a
+// block for every chunk (the grid holds at least one block a group). Returns false for a block past the chunks.
+template <int TILES> __device__ __forceinline__ bool group_chunk(int groups, int& g, int& first, int& last) {
+  int per = max(1, (groups * TILES + (int)gridDim.x - 1) / (int)gridDim.x);
+  while (per < TILES && groups * ((TILES + per - 1) / per) > (int)gridDim.x) ++per;
+  const int cpg = (TILES + per - 1) / per;
+  g = blockIdx.x / cpg;
+  const int c = blockIdx.x - g * cpg;
+  first = g * TILES + c * per;
+  last = g * TILES + min(TILES, (c + 1) * per);
+  return g < groups;
+}
+
 // an item in LDS: 16 rows of gate then 16 of up at a padded stride, as 16-byte chunks; wave w loads the runs of 64
 // chunks w, w + 8, ... (the last run's chunks past the item re-read its last chunk into the slot's tail)
 template <int KIND> struct FrontItem {
@@ -360,6 +440,8 @@ __global__ __launch_bounds__(FRONT_WAVES * 64) void k_moe_front(
   __shared__ int s_gexp[MOE_MAX_PAIRS + 1];
   __shared__ int s_groups;
   __shared__ int s_wp[FRONT_WAVES][16];
+  __shared__ key_t s_tk[FRONT_WAVES][2][16];
+  __shared__ float s_ev[FRONT_WAVES][16];
 
   // the IQ3_S table first: it does not wait on the choice (2048 chunks, four a thread)
   if constexpr (KIND == IQ3_S) {
@@ -371,7 +453,8 @@ __global__ __launch_bounds__(FRONT_WAVES * 64) void k_moe_front(
   }
   if (tid < WORDS) s_flag[tid] = 0u;
 
-  // 1. each token's top-k of the logits and the softmax of the chosen (a wave a token, its logits loaded first)
+  // 1. each token's top-k of the logits and the softmax of the chosen (a wave a token, its logits loaded first);
+  // the chosen experts flagged as they are found
   {
     key_t key[2][VPL];
 #pragma unroll
@@ -382,33 +465,28 @@ __global__ __launch_bounds__(FRONT_WAVES * 64) void k_moe_front(
         for (int i = 0; i < VPL; ++i) key[u][i] = RK::make(logits[(int64_t)t * E + i * 64 + lane], i * 64 + lane);
       }
     }
+    lds_sync();  // the flags cleared (the loads stay in flight)
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
       const int t = wave + FRONT_WAVES * u;
       if (t >= B) break;
-      float top = 0.0f, sum = 0.0f, my_e = 0.0f;
-      for (int r = 0; r < K; ++r) {
-        key_t best = key[u][0];
-#pragma unroll
-        for (int i = 1; i < VPL; ++i) best = key[u][i] > best ? key[u][i] : best;
-        best = RK::wave_max(best);
-        const float v = RK::value(best);
-        if (r == 0) top = v;
-        const float ev = expf(v - top);
-        sum += ev;
-        if (lane == r) {
-          my_e = ev;
-          s_idx[t * K + r] = RK::index(best);
-        }
-#pragma unroll
-        for (int i = 0; i < VPL; ++i)
-          if (key[u][i] == best) key[u][i] = 0;
+      wave_top_k<RK, VPL>(key[u], K, s_tk[wave][0], s_tk[wave][1]);
+      // the softmax of the chosen in rank order, as the reference sums it
+      const key_t* sorted = s_tk[wave][1];
+      const float top = RK::value(sorted[0]);
+      if (lane < K) s_ev[wave][lane] = expf(RK::value(sorted[lane]) - top);
+      __builtin_amdgcn_wave_barrier();
+      float sum = 0.0f;
+      for (int r = 0; r < K; ++r) sum += s_ev[wave][r];
+      if (lane < K) {
+        const int e = RK::index(sorted[lane]);
+        s_idx[t * K + lane] = e;
+        s_wt[t * K + lane] = s_ev[wave][lane] / sum;
+        atomicOr(&s_flag[e >> 5], 1u << (e & 31));
       }
-      if (lane < K) s_wt[t * K + lane] = my_e / sum;
+      __builtin_amdgcn_wave_barrier();
     }
   }
-  __syncthreads();
-  if (tid < P) atomicOr(&s_flag[s_idx[tid] >> 5], 1u << (s_idx[tid] & 31));
   __syncthreads();
   // 2. the groups: the chosen experts in ascending order, then the shared expert
   if (wave == 0) {
@@ -459,11 +537,9 @@ __global__ __launch_bounds__(FRONT_WAVES * 64) void k_moe_front(
     }
   }
 
-  // 3. this block's run of the items
-  const int items = groups * TILES;
-  const int per = (items + gridDim.x - 1) / gridDim.x;
-  const int first = blockIdx.x * per, last = min(items, first + per);
-  if (first >= last) return;  // block-uniform
+  // 3. this block's run of the items: part of one group's
+  int g0, first, last;
+  if (!group_chunk<TILES>(groups, g0, first, last)) return;  // block-uniform
 
   // this thread's chunks of an item: matrix (0 gate, 1 up) and byte offset from the item's first row; the slot's
   // tail past the two matrices re-reads up's last chunk. Each wave waits on its own count of loads.
@@ -479,20 +555,32 @@ __global__ __launch_bounds__(FRONT_WAVES * 64) void k_moe_front(
     pre_off[j] = m >= 2 ? 15 * RB + 16 * (IT::CPR_SRC - 1) : row * RB + 16 * min(kk, IT::CPR_SRC - 1);
   }
   const int64_t ebytes = (int64_t)F * RB;
+  const int e0 = s_gexp[g0];
+  const uint8_t* gate_e = e0 == E ? sh_gate : gate + (int64_t)e0 * ebytes;
+  const uint8_t* up_e = e0 == E ? sh_up : up + (int64_t)e0 * ebytes;
   auto issue = [&](int item) {
-    const int g = item / TILES, r = item - g * TILES;
-    const int e = s_gexp[g];
-    const uint8_t* gs = (e == E ? sh_gate : gate + (int64_t)e * ebytes) + (int64_t)r * 16 * RB;
-    const uint8_t* us = (e == E ? sh_up : up + (int64_t)e * ebytes) + (int64_t)r * 16 * RB;
+    const int r = item - g0 * TILES;
+    const uint8_t* gs = gate_e + (int64_t)r * 16 * RB;
+    const uint8_t* us = up_e + (int64_t)r * 16 * RB;
     const uint32_t buf = lds_base + fp.ring_off + (item % fp.nbuf) * IT::SLOT + wave * 1024;
 #pragma unroll
     for (int j = 0; j < IT::LOADS; ++j)
       if (j < loads) lds_dma16p((pre_up[j] ? us : gs) + pre_off[j], buf + j * (NT * 16));
   };
+  // the group's tokens and their activation loads, then the ring's first items: both in flight at once
+  const int n_tok = group_pairs(e0, E, s_idx, B, K, s_wp[wave]);
+  XRaw<KIND, GPER> xraw;
+  {
+    int mt = lane_token<TPG>();
+    mt = mt < n_tok ? mt : 0;
+    const int pp = s_wp[wave][mt];
+    x_issue<KIND, XT, GPER>(xraw, x + (int64_t)(pp < P ? pp / K : pp - P) * D, kq * GPER);
+  }
   for (int k = 0; k < fp.nbuf - 1 && first + k < last; ++k) issue(first + k);
+  XRegs<KIND, TPG, GPER> X;
+  x_finish<KIND, XT, TPG, GPER>(X, xraw);
 
   const DecodeRegs kr = decode_regs<KIND, MT>();
-  XRegs<KIND, TPG, GPER> X;
   const int wcol = KIND == Q2_0 ? kq * GPER * 18 : (kq * GPER / 8) * 110;  // the wave's first group in a row
   constexpr int RED = 7 * 64 * TPG;  // up's partial sums after gate's
   // an item's results are stored at the start of the next (after that item's wait: see the streaming matvec)
@@ -505,35 +593,13 @@ __global__ __launch_bounds__(FRONT_WAVES * 64) void k_moe_front(
         if (hp[t] >= 0) ((XT*)ws.h)[(int64_t)hp[t] * F + hrow] = hv[t];
     }
   };
-  int g_cur = -1, n_tok = 0;
   for (int item = first; item < last; ++item) {
     const int ahead = min(fp.nbuf - 2, last - 1 - item);  // items issued after this one
     wait_vmcnt(ahead * loads);
     lds_sync();  // this item is in LDS for every wave; every wave is done with the item before
     store_h();
     if (item + fp.nbuf - 1 < last) issue(item + fp.nbuf - 1);
-    const int g = item / TILES, r = item - g * TILES;
-    if (g != g_cur) {  // a new group: its tokens in token order (each wave for itself), their fragments
-      g_cur = g;
-      const int e = s_gexp[g];
-      if (e < E) {
-        int jh = -1;
-        if (lane < B)
-          for (int j = 0; j < K; ++j)
-            if (s_idx[lane * K + j] == e) jh = j;
-        const uint64_t bal = __ballot(jh >= 0);
-        n_tok = __popcll(bal);
-        if (jh >= 0) s_wp[wave][__popcll(bal & ((1ull << lane) - 1ull))] = lane * K + jh;
-      } else {
-        n_tok = B;
-        if (lane < B) s_wp[wave][lane] = P + lane;
-      }
-      __builtin_amdgcn_wave_barrier();
-      int mt = lane_token<TPG>();
-      mt = mt < n_tok ? mt : 0;
-      const int pp = s_wp[wave][mt];
-      load_x_row<KIND, XT, TPG, GPER, true>(X, x + (int64_t)(pp < P ? pp / K : pp - P) * D, kq * GPER);
-    }
+    const int r = item - g0 * TILES;
     float acc_g[TPG], acc_u[TPG];
 #pragma unroll
     for (int t = 0; t < TPG; ++t) acc_g[t] = acc_u[t] = 0.0f;
@@ -628,28 +694,35 @@ __global__ __launch_bounds__(FRONT_WAVES * 64) void k_moe_tail(const uint8_t* __
   if (tid <= P) s_gexp[tid] = ws.g_expert[tid];  // entries past the groups are never read
   __syncthreads();
   const int groups = s_groups;
-  const int items = groups * TILES;
-  const int per = (items + gridDim.x - 1) / gridDim.x;
-  const int first = blockIdx.x * per, last = min(items, first + per);
-  if (first >= last) return;  // block-uniform; the barrier above waited for the table
+  int g0, first, last;  // this block's run of items: part of one group's
+  if (!group_chunk<TILES>(groups, g0, first, last)) return;  // block-uniform; the barrier above waited for the table
 
   const int loads = (IT::RUNS - wave + FRONT_WAVES - 1) / FRONT_WAVES;
   int pre_off[IT::LOADS];
 #pragma unroll
   for (int j = 0; j < IT::LOADS; ++j) pre_off[j] = 16 * min((j * FRONT_WAVES + wave) * 64 + lane, IT::CHUNKS - 1);
+  const int e0 = s_gexp[g0];
+  const uint8_t* down_e = e0 == E ? sh_down : down + (int64_t)e0 * D * RB;
   auto issue = [&](int item) {
-    const int g = item / TILES, tile = item - g * TILES;
-    const int e = __builtin_amdgcn_readfirstlane(s_gexp[g]);  // block-uniform: a scalar base
-    const uint8_t* src = (e == E ? sh_down : down + (int64_t)e * D * RB) + (int64_t)tile * IT::ROWS * RB;
+    const uint8_t* src = down_e + (int64_t)(item - g0 * TILES) * IT::ROWS * RB;
     const uint32_t buf = lds_base + tp.ring_off + (item % tp.nbuf) * IT::SLOT + wave * 1024;
 #pragma unroll
     for (int j = 0; j < IT::LOADS; ++j)
       if (j < loads) lds_dma16(src, pre_off[j], buf + j * (NT * 16));
   };
+  // the group's tokens and their loads of h, then the ring's first items: both in flight at once
+  const int n_tok = group_pairs(e0, E, s_idx, B, K, s_wp[wave]);
+  XRaw<KIND, GPER> xraw;
+  {
+    int mt = lane_token<TPG>();
+    mt = mt < n_tok ? mt : 0;
+    x_issue<KIND, XT, GPER>(xraw, (const XT*)ws.h + (int64_t)s_wp[wave][mt] * F, kh * GPER);
+  }
   for (int k = 0; k < tp.nbuf - 1 && first + k < last; ++k) issue(first + k);
+  XRegs<KIND, TPG, GPER> X;
+  x_finish<KIND, XT, TPG, GPER>(X, xraw);
 
   const DecodeRegs kr = decode_regs<KIND, MT>();
-  XRegs<KIND, TPG, GPER> X;
   // each pair's outputs, rounded to the activation type, go out as device-scope stores (through the XCD's L2 to
   // memory) at the start of the next item
   float yv[TPG];
@@ -662,34 +735,13 @@ __global__ __launch_bounds__(FRONT_WAVES * 64) void k_moe_tail(const uint8_t* __
           __hip_atomic_store(&ws.y[(int64_t)yp[t] * D + yrow], yv[t], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
   };
-  int g_cur = -1, n_tok = 0;
   for (int item = first; item < last; ++item) {
     const int ahead = min(tp.nbuf - 2, last - 1 - item);
     wait_vmcnt(ahead * loads);
     lds_sync();
     store_y();
     if (item + tp.nbuf - 1 < last) issue(item + tp.nbuf - 1);
-    const int g = item / TILES, tile = item - g * TILES;
-    if (g != g_cur) {  // a new group: its tokens in token order (each wave for itself), their fragments of h
-      g_cur = g;
-      const int e = s_gexp[g];
-      if (e < E) {
-        int jh = -1;
-        if (lane < B)
-          for (int j = 0; j < K; ++j)
-            if (s_idx[lane * K + j] == e) jh = j;
-        const uint64_t bal = __ballot(jh >= 0);
-        n_tok = __popcll(bal);
-        if (jh >= 0) s_wp[wave][__popcll(bal & ((1ull << lane) - 1ull))] = lane * K + jh;
-      } else {
-        n_tok = B;
-        if (lane < B) s_wp[wave][lane] = P + lane;
-      }
-      __builtin_amdgcn_wave_barrier();
-      int mt = lane_token<TPG>();
-      mt = mt < n_tok ? mt : 0;
-      load_x_row<KIND, XT, TPG, GPER, true>(X, (const XT*)ws.h + (int64_t)s_wp[wave][mt] * F, kh * GPER);
-    }
+    const int tile = item - g0 * TILES;
     float acc[TPG];
 #pragma unroll
     for (int t = 0; t < TPG; ++t) acc[t] = 0.0f;
@@ -726,42 +778,41 @@ __global__ __launch_bounds__(FRONT_WAVES * 64) void k_moe_tail(const uint8_t* __
   }
   __syncthreads();
   const int ncomb = s_ncomb;
-  // the combine (strata_mlx/fused.py:448-462): experts in 8 rows j taking k = j, j + 8, ..., each product rounded
-  for (int c = 0; c < ncomb; ++c) {
-    const int tile = s_comb[c];
-    for (int qv = tid; qv < B * IT::ROWS; qv += NT) {
-      const int t = qv / IT::ROWS, row = tile * IT::ROWS + qv % IT::ROWS;
-      float y[16], w[16];  // k <= 16
+  // the combine (strata_mlx/fused.py:448-462): experts in 8 rows j taking k = j, j + 8, ..., each product rounded;
+  // every (tile, token, row) of the block's tiles at once, so their loads go out together
+  for (int qv = tid; qv < ncomb * B * IT::ROWS; qv += NT) {
+    const int c = qv / (B * IT::ROWS), rest = qv - c * (B * IT::ROWS);
+    const int t = rest / IT::ROWS, row = s_comb[c] * IT::ROWS + rest % IT::ROWS;
+    float y[16], w[16];  // k <= 16
 #pragma unroll
-      for (int kk = 0; kk < 16; ++kk) {
-        y[kk] = kk < K ? __hip_atomic_load(&ws.y[(int64_t)(t * K + kk) * D + row], __ATOMIC_RELAXED,
-                                           __HIP_MEMORY_SCOPE_AGENT) : 0.0f;
-        w[kk] = kk < K ? ws.w[t * K + kk] : 0.0f;
-      }
-      const float ys = __hip_atomic_load(&ws.y[(int64_t)(P + t) * D + row], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      float acc2 = 0.0f;
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        if (j < K) {
-          float part = 0.0f;
-#pragma unroll
-          for (int i = 0; i < 2; ++i) {
-            const int kk = j + 8 * i;
-            if (kk < K) {
-              const float prod = y[kk] * w[kk];
-              part = prod + part;
-            }
-          }
-          acc2 = j == 0 ? part : part + acc2;
-        }
-      }
-      const XT routed = from_f32<XT>(acc2);
-      const XT gate = from_f32<XT>(1.0f / (1.0f + expf(-ws.gsh[t])));
-      const XT shared = from_f32<XT>(to_f32(gate) * ys);
-      out[(int64_t)t * D + row] = from_f32<XT>(to_f32(routed) + to_f32(shared));
+    for (int kk = 0; kk < 16; ++kk) {
+      y[kk] = kk < K ? __hip_atomic_load(&ws.y[(int64_t)(t * K + kk) * D + row], __ATOMIC_RELAXED,
+                                         __HIP_MEMORY_SCOPE_AGENT) : 0.0f;
+      w[kk] = kk < K ? ws.w[t * K + kk] : 0.0f;
     }
-    if (tid == 0) __hip_atomic_store(&ws.cnt[tile], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const float ys = __hip_atomic_load(&ws.y[(int64_t)(P + t) * D + row], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    float acc2 = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      if (j < K) {
+        float part = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+          const int kk = j + 8 * i;
+          if (kk < K) {
+            const float prod = y[kk] * w[kk];
+            part = prod + part;
+          }
+        }
+        acc2 = j == 0 ? part : part + acc2;
+      }
+    }
+    const XT routed = from_f32<XT>(acc2);
+    const XT gate = from_f32<XT>(1.0f / (1.0f + expf(-ws.gsh[t])));
+    const XT shared = from_f32<XT>(to_f32(gate) * ys);
+    out[(int64_t)t * D + row] = from_f32<XT>(to_f32(routed) + to_f32(shared));
   }
+  if (tid < ncomb) __hip_atomic_store(&ws.cnt[s_comb[tid]], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // ---- down and the combine: a block is 16 output rows of every group's expert
@@ -961,6 +1012,8 @@ static int launch_moe(const uint8_t* gate, const uint8_t* up, const uint8_t* dow
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, nt, lds) != hipSuccess || per_cu < 1) per_cu = 1;
     const int64_t most = (std::min<int64_t>(B * K, E) + 1) * (FRONT_F / 16);
     const int64_t grid = std::min<int64_t>(most, (int64_t)device_cus() * per_cu);
+    if (grid < std::min<int64_t>(B * K, E) + 1)  // a block at least for each group
+      return fail(E_UNSUPPORTED, "moe_decode: %lld blocks for the front", (long long)grid);
     hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(nt), lds, stream, gate, up, sg, su, logits, x, wg, (int)K,
                        (int)B, fp, stab, ws);
     st = check_launch("moe_decode front");
@@ -986,8 +1039,8 @@ static int launch_moe(const uint8_t* gate, const uint8_t* up, const uint8_t* dow
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, nt, lds) != hipSuccess || per_cu < 1) per_cu = 1;
     const int64_t most = (std::min<int64_t>(B * K, E) + 1) * IT::TILES;
     const int64_t grid = std::min<int64_t>(most, (int64_t)device_cus() * per_cu);
-    if ((most + grid - 1) / grid > MOE_MAX_PAIRS)  // a block's items, each counted by a thread of its own
-      return fail(E_UNSUPPORTED, "moe_decode: %lld tail items a block", (long long)((most + grid - 1) / grid));
+    if (grid < std::min<int64_t>(B * K, E) + 1)  // a block at least for each group (a block's items are then at
+      return fail(E_UNSUPPORTED, "moe_decode: %lld blocks for the tail", (long long)grid);  // most TILES)
     hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(nt), lds, stream, down, sd, (int)K, (int)B, tp, stab, ws, out);
     st = check_launch("moe_decode tail");
     if (st) return st;

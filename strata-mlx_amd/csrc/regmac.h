@@ -42,42 +42,93 @@ template <int KIND, int TPG, int GPER> struct XRegs {
   float nc[GPER][TPG];
 };
 
-// XRegs for scale groups [gbase, gbase + GPER) of the lane's activation row xr (the row of its A-row token).
-// Q2_0: lane g's fragment a takes block-local weights k = 32h + 8g + 4a + j (j < 4, h < 2) into slot 2j + h, scaled
-// by 1 / U_j (the in-place mask's unit), as XStage stages them, or as they are with RAW (for item_mac's RAW decode,
-// which shifts each code down to bit 0 instead); IQ3_S: values 8g..8g+7 of the run as they are. The sums: each
-// lane's share, added over the four lanes of a row (xor 16, 32), then fetched from a lane whose A-row is the wanted
-// token (lane 4g + t holds token g * TPG + t).
-template <int KIND, typename XT, int TPG, int GPER, bool RAW = false>
-__device__ __forceinline__ void load_x_row(XRegs<KIND, TPG, GPER>& X, const XT* xr, int gbase) {
-  using MT = XT;
-  const int lane = threadIdx.x & 63, g = lane >> 4;
-  float part[GPER];
-  if constexpr (KIND == Q2_0 && RAW) {
-    u32x4 v[GPER][2];
+// A wave's activation row loads for its GPER scale groups as they lie (lane g: Q2_0 values 8g..8g+7 and
+// 32+8g..32+8g+7 of each block, IQ3_S values 8g..8g+7 of each run), issued by x_issue and turned into XRegs by
+// x_finish: a caller can put other loads in flight between the two.
+template <int KIND, int GPER> struct XRaw {
+  u32x4 v[GPER][KIND == Q2_0 ? 2 : 1];
+};
+
+template <int KIND, typename XT, int GPER>
+__device__ __forceinline__ void x_issue(XRaw<KIND, GPER>& R, const XT* xr, int gbase) {
+  const int g = (threadIdx.x & 63) >> 4;
 #pragma unroll
-    for (int j = 0; j < GPER; ++j) {
-      v[j][0] = *(const u32x4*)(xr + (gbase + j) * 64 + 8 * g);
-      v[j][1] = *(const u32x4*)(xr + (gbase + j) * 64 + 32 + 8 * g);
+  for (int j = 0; j < GPER; ++j) {
+    if constexpr (KIND == Q2_0) {
+      R.v[j][0] = *(const u32x4*)(xr + (gbase + j) * 64 + 8 * g);
+      R.v[j][1] = *(const u32x4*)(xr + (gbase + j) * 64 + 32 + 8 * g);
+    } else {
+      R.v[j][0] = *(const u32x4*)(xr + (gbase + j) * 32 + 8 * g);
     }
+  }
+}
+
+// minus each group's offset sum for the TPG tokens of the lane's D-rows: the lane's share, added over the four
+// lanes of a row (xor 16, 32), then fetched from a lane whose A-row is the wanted token (lane 4g + t holds token
+// g * TPG + t)
+template <int TPG, int GPER>
+__device__ __forceinline__ void x_sums(float (&nc)[GPER][TPG], const float (&part)[GPER]) {
+  const int g = (threadIdx.x & 63) >> 4;
 #pragma unroll
-    for (int j = 0; j < GPER; ++j) {
+  for (int j = 0; j < GPER; ++j) {
+    float p = part[j];
+    p += __shfl_xor(p, 16);
+    p += __shfl_xor(p, 32);
+#pragma unroll
+    for (int t = 0; t < TPG; ++t) nc[j][t] = -__shfl(p, 4 * g + t);
+  }
+}
+
+// XRegs from raw loads, activations as they are: Q2_0 lane g's fragment a takes block-local weights
+// k = 32h + 8g + 4a + j (j < 4, h < 2) into slot 2j + h (for item_mac's RAW decode, which shifts each code down to
+// bit 0); IQ3_S the run's values 8g..8g+7
+template <int KIND, typename XT, int TPG, int GPER>
+__device__ __forceinline__ void x_finish(XRegs<KIND, TPG, GPER>& X, const XRaw<KIND, GPER>& R) {
+  using MT = XT;
+  float part[GPER];
+#pragma unroll
+  for (int j = 0; j < GPER; ++j) {
+    if constexpr (KIND == Q2_0) {
       // slot 2j + h of fragment a: x[32h + 8g + 4a + j], so each dword pairs a half of v[j][0] with the same half
       // of v[j][1]
-      const uint32_t a0[4] = {v[j][0].x, v[j][0].y, v[j][0].z, v[j][0].w};
-      const uint32_t a1[4] = {v[j][1].x, v[j][1].y, v[j][1].z, v[j][1].w};
+      const uint32_t a0[4] = {R.v[j][0].x, R.v[j][0].y, R.v[j][0].z, R.v[j][0].w};
+      const uint32_t a1[4] = {R.v[j][1].x, R.v[j][1].y, R.v[j][1].z, R.v[j][1].w};
       X.xa[j] = u32x4{__builtin_amdgcn_perm(a1[0], a0[0], 0x05040100u), __builtin_amdgcn_perm(a1[0], a0[0], 0x07060302u),
                       __builtin_amdgcn_perm(a1[1], a0[1], 0x05040100u), __builtin_amdgcn_perm(a1[1], a0[1], 0x07060302u)};
       X.xb[j] = u32x4{__builtin_amdgcn_perm(a1[2], a0[2], 0x05040100u), __builtin_amdgcn_perm(a1[2], a0[2], 0x07060302u),
                       __builtin_amdgcn_perm(a1[3], a0[3], 0x05040100u), __builtin_amdgcn_perm(a1[3], a0[3], 0x07060302u)};
-      const XT* h0 = (const XT*)&v[j][0];
-      const XT* h1 = (const XT*)&v[j][1];
+      const XT* h0 = (const XT*)&R.v[j][0];
+      const XT* h1 = (const XT*)&R.v[j][1];
       float p = 0.0f;
 #pragma unroll
       for (int i = 0; i < 8; ++i) p += to_f32(h0[i]) + to_f32(h1[i]);
       part[j] = (Magic<MT>::BASE + 1.0f) * p;
+    } else {
+      X.xa[j] = R.v[j][0];
+      const XT* e = (const XT*)&R.v[j][0];
+      float p = 0.0f;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) p += to_f32(e[i]);
+      part[j] = (Magic<MT>::BASE + 16.0f) * p;
     }
-  } else if constexpr (KIND == Q2_0) {
+  }
+  x_sums<TPG, GPER>(X.nc, part);
+}
+
+// XRegs for scale groups [gbase, gbase + GPER) of the lane's activation row xr (the row of its A-row token).
+// Q2_0: lane g's fragment a takes block-local weights k = 32h + 8g + 4a + j (j < 4, h < 2) into slot 2j + h, scaled
+// by 1 / U_j (the in-place mask's unit), as XStage stages them, or as they are with RAW (x_finish); IQ3_S: values
+// 8g..8g+7 of the run as they are.
+template <int KIND, typename XT, int TPG, int GPER, bool RAW = false>
+__device__ __forceinline__ void load_x_row(XRegs<KIND, TPG, GPER>& X, const XT* xr, int gbase) {
+  using MT = XT;
+  if constexpr (KIND != Q2_0 || RAW) {
+    XRaw<KIND, GPER> R;
+    x_issue<KIND, XT, GPER>(R, xr, gbase);
+    x_finish<KIND, XT, TPG, GPER>(X, R);
+  } else {
+    const int lane = threadIdx.x & 63, g = lane >> 4;
+    float part[GPER];
     u32x4 v[GPER][2];
 #pragma unroll
     for (int j = 0; j < GPER; ++j) {
@@ -104,25 +155,7 @@ __device__ __forceinline__ void load_x_row(XRegs<KIND, TPG, GPER>& X, const XT* 
       X.xb[j] = u32x4{w[1][0], w[1][1], w[1][2], w[1][3]};
       part[j] = p;
     }
-  } else {
-#pragma unroll
-    for (int j = 0; j < GPER; ++j) X.xa[j] = *(const u32x4*)(xr + (gbase + j) * 32 + 8 * g);
-#pragma unroll
-    for (int j = 0; j < GPER; ++j) {
-      const XT* e = (const XT*)&X.xa[j];
-      float p = 0.0f;
-#pragma unroll
-      for (int i = 0; i < 8; ++i) p += to_f32(e[i]);
-      part[j] = (Magic<MT>::BASE + 16.0f) * p;
-    }
-  }
-#pragma unroll
-  for (int j = 0; j < GPER; ++j) {
-    float p = part[j];
-    p += __shfl_xor(p, 16);
-    p += __shfl_xor(p, 32);
-#pragma unroll
-    for (int t = 0; t < TPG; ++t) X.nc[j][t] = -__shfl(p, 4 * g + t);
+    x_sums<TPG, GPER>(X.nc, part);
   }
 }
 

@@ -110,7 +110,13 @@ __device__ __forceinline__ int lead_of(const void* p) { return (int)((uintptr_t)
 // insertion, which would count such a load as pending on the LDS counter too and then wait for every LDS read at
 // once, does not see it (its own waits on younger loads stay correct: the counter drains in order).
 __device__ __forceinline__ void lds_dma16(const void* base, uint32_t off, uint32_t lds) {
-  asm volatile("global_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base), "{m0}"(__builtin_amdgcn_readfirstlane(lds))
+  // the base is wave-uniform by contract: read from the first lane, it is a scalar operand whatever the compiler
+  // could prove
+  const uint64_t b = (uint64_t)(uintptr_t)base;
+  const uint64_t sb = ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(b >> 32)) << 32) |
+                      (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)b);
+  asm volatile("global_load_lds_dwordx4 %0, %1" ::"v"(off), "s"((const void*)(uintptr_t)sb),
+               "{m0}"(__builtin_amdgcn_readfirstlane(lds))
                : "memory");
 }
 // the same with a full address a lane (sources in different tensors within one wave's load)
