@@ -10,9 +10,12 @@ value = algorithmic bytes of all timed layers / their time, where a layer's byte
 tokens actually chose (counted from the routing) plus the shared expert, plus activations in and out:
 (U + 1) * 884,736 + B * 9,216 + 4,096.
 
-roofline: the dominant kernel (gate/up with SwiGLU, two thirds of the expert bytes), its launches timed by HIP
-events around a graph of them alone. cpu_baseline: the numpy oracle's restatement of the reference's dequantize +
-matmul path on the host, one thread, over a bounded sample of the same layers.
+roofline: the dominant kernel, k_moe_front (route, then gate/up with SwiGLU: two thirds of the expert bytes), its
+launches timed by HIP events around a graph of them alone; its algorithmic bytes are the gate and up blocks of the
+chosen and the shared experts, the logits and hidden states in, swiglu(gate, up) out. traffic: the HBM bytes a
+launch moves by the FETCH_SIZE / WRITE_SIZE counters (profiles/moe_front_traffic.json, made by
+strata-mlx_amd/strata_hip/profile_traffic.py under rocprofv3). cpu_baseline: the numpy oracle's restatement of the
+reference's dequantize + matmul path on the host, one thread, over a bounded sample of the same layers.
 
     python bench.py [--steps K] [--warmup W] [--layers 48] [--batches 1,2,4,8] [--no-cpu]
 """
@@ -38,9 +41,19 @@ def layer_bytes(u: int, b: int) -> int:
     return (u + 1) * EXPERT_BYTES + b * 9_216 + 4_096
 
 
-def gate_up_bytes(u: int, b: int) -> int:
-    # gate + up blocks of the chosen and the shared experts, x in, swiglu(gate, up) out
-    return (u + 1) * 2 * 294_912 + b * D * 2 + (b * K + b) * F * 2
+def front_bytes(u: int, b: int) -> int:
+    # gate + up blocks of the chosen and the shared experts, logits and x in, swiglu(gate, up) out
+    return (u + 1) * 2 * 294_912 + b * E * 2 + b * D * 2 + (b * K + b) * F * 2
+
+
+def front_traffic():
+    """HBM bytes a k_moe_front launch moves, averaged over the batches the counters were read at (None without the
+    committed counter summary)."""
+    path = os.path.join(ROOT, "profiles", "moe_front_traffic.json")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        return json.load(f).get("traffic_bytes_per_launch")
 
 
 def build_layers(n_layers, dev, kind):
@@ -337,9 +350,8 @@ def main():
             with torch.cuda.graph(graph, stream=stream):
                 for m, lg, x, o in zip(layers, logits, xs, outs):
                     m(lg, x, out=o)
-            # the dominant kernel alone: every layer routed once, then a graph of the gate/up launches only
-            for m, lg, x, o in zip(layers, logits, xs, outs):
-                m(lg, x, phase=0)
+            # the dominant kernel alone: a graph of the front launches only (route, gate and up; the MoE path's
+            # phases 0 and 1 are both this kernel for this shape)
             gu_graph = torch.cuda.CUDAGraph()
             with torch.cuda.graph(gu_graph, stream=stream):
                 for m, lg, x, o in zip(layers, logits, xs, outs):
@@ -358,7 +370,7 @@ def main():
                 gu_graph.replay()
             ev[3].record(stream)
             torch.cuda.synchronize()
-            # leave the outputs of a full pass behind (the gate/up graph rewrote h, not the outputs)
+            # leave the outputs of a full pass behind (the front's graph rewrote h, not the outputs)
             graph.replay()
             torch.cuda.synchronize()
         ms = ev[0].elapsed_time(ev[1])
@@ -368,10 +380,10 @@ def main():
                         "GBps": round(bytes_pass * args.steps / (ms * 1e-3) / 1e9, 1),
                         "unique_experts_mean": round(float(np.mean(uniq)), 2),
                         "tok_per_s": round(b * args.steps / (ms * 1e-3), 1),
-                        "gate_up_us": round(gu_ms * 1e3 / n_layers, 3)}
+                        "front_us": round(gu_ms * 1e3 / n_layers, 3)}
         all_bytes += bytes_pass * args.steps
         all_time += ms * 1e-3
-        gu_bytes += sum(gate_up_bytes(u, b) for u in uniq) * args.steps
+        gu_bytes += sum(front_bytes(u, b) for u in uniq) * args.steps
         gu_time += gu_ms * 1e-3
         gu_launches += n_layers
         inputs[b] = list(zip(logits, xs, outs))
@@ -382,7 +394,7 @@ def main():
     prefill = None if args.no_prefill else prefill_layer(dev, max(3, args.steps // 4), args.warmup)
     value = all_bytes / all_time / 1e9
     achieved = gu_bytes / gu_time / 1e9
-    traffic = None
+    traffic = front_traffic()
     cpu = None
     if not args.no_cpu:
         gbs, secs, n_done, n_layers_used, checks = cpu_baseline(raw, inputs, args.kind, args.cpu_seconds, True)
@@ -402,7 +414,7 @@ def main():
         "paged_attention": attention,
         "prefill_layer": prefill,
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic, "kernel": "k_moe_gate_up",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic, "kernel": "k_moe_front",
                      "bytes_per_launch": round(gu_bytes / gu_launches), "launches": gu_launches,
                      "us_per_launch": round(gu_time * 1e6 / gu_launches, 3)},
         "cpu_baseline": cpu,

@@ -80,9 +80,15 @@ def test_hip_path_matches_the_fixtures(fx, tables, dev):
     shapes = {"gate": (E, F, D), "up": (E, F, D), "down": (E, D, F), "sgate": (1, F, D), "sup": (1, F, D),
               "sdown": (1, D, F)}
     lin = {n: SB.BlockSwitchLinear(torch.from_numpy(fx[f"moe/{n}"]).to(dev), "Q2_0", shapes[n]) for n in shapes}
-    moe = SF.MoEDecode(lin["gate"], lin["up"], lin["down"], lin["sgate"], lin["sup"], lin["sdown"],
-                       bf(fx["moe/shared_gate_w"]), K)
-    out, oidx, ow = moe(bf(fx["moe/logits"]), bf(fx["moe/x"]), want_choice=True)
+    # the block of 8 experts through the reference's composition (strata_mlx/fused.py:484-497): top-k, switch_glu
+    # of the routed and of the shared expert, the shared gate's logit rounded to bf16, moe_combine
+    x = bf(fx["moe/x"])
+    oidx, ow = SF.top_k(bf(fx["moe/logits"]), K, weights=True)
     np.testing.assert_array_equal(oidx.cpu().numpy(), fx["moe/idx"])
     np.testing.assert_allclose(ow.cpu().numpy(), fx["moe/weights"], rtol=2e-6, atol=1e-7)
+    y = SB.BlockSwitchGLU(lin["gate"], lin["up"], lin["down"])(x, oidx)
+    zero = torch.zeros((x.shape[0], 1), dtype=torch.int32, device=dev)
+    sh = SB.BlockSwitchGLU(lin["sgate"], lin["sup"], lin["sdown"])(x, zero)[:, 0, :]
+    g = (x.float() @ bf(fx["moe/shared_gate_w"]).float()).to(torch.bfloat16)
+    out = SF.moe_combine(y, ow, g[:, None], sh)
     assert rel_err(out.float().cpu(), fx["moe/out"]) <= 1e-2
