@@ -133,17 +133,21 @@ int sh_tiles_of(const int32_t* idx, int64_t pairs, int64_t k, int64_t experts, i
  * router logits (float32 or the activation dtype; ties to the lower index) and the softmax of the chosen ones
  * (fused.py:491); gate/up/down of each token's experts read straight from the GGUF stacks, SwiGLU with the
  * reference's roundings (strata_mlx/blocks.py:819-829); the shared expert and its gate x . shared_gate_w; the
- * combine (fused.py:448-481). Three kernels, no host synchronisation. kind / kind_down: Q2_0 or IQ3_S; dtype: F16
- * or BF16; d_model, d_ff multiples of 256; experts a multiple of 64 up to 2048. idx_out (tokens x k int32) and
- * w_out (tokens x k float32) are optional copies of the choice. workspace: sh_moe_workspace() bytes. */
+ * combine (fused.py:448-481). No host synchronisation: for 512 experts, d_model 2048, d_ff 512 (16-byte aligned
+ * operands) two kernels (route + gate/up + SwiGLU; down + combine), otherwise three (route; gate/up; down +
+ * combine). kind / kind_down: Q2_0 or IQ3_S; dtype: F16 or BF16; d_model, d_ff multiples of 256; experts a multiple
+ * of 64 up to 2048. idx_out (tokens x k int32) and w_out (tokens x k float32) are optional copies of the choice.
+ * workspace: sh_moe_workspace() bytes, zeroed once before its first call (it holds counters that every call leaves
+ * at zero); calls sharing a workspace must not overlap. */
 size_t sh_moe_workspace(int64_t tokens, int64_t k, int64_t d_model, int64_t d_ff, int dtype);
 int sh_moe_decode(int kind, int kind_down, const void* gate, const void* up, const void* down, int64_t experts,
                   const void* shared_gate, const void* shared_up, const void* shared_down, const void* shared_gate_w,
                   const void* tables, const void* logits, int logits_dtype, const void* x, int dtype, int64_t tokens,
                   int64_t k, int64_t d_model, int64_t d_ff, void* out, int32_t* idx_out, float* w_out,
                   void* workspace, size_t workspace_bytes, void* stream);
-/* One of sh_moe_decode's three kernels alone (phase 0 route, 1 gate/up, 2 down + combine), in that order over one
- * workspace: what a caller times or interleaves kernel by kernel. */
+/* One of sh_moe_decode's kernels alone (phase 0 route, 1 gate/up, 2 down + combine; for the two-kernel shape
+ * phases 0 and 1 are both the route + gate/up kernel), in that order over one workspace: what a caller times or
+ * interleaves kernel by kernel. */
 int sh_moe_decode_phase(int phase, int kind, int kind_down, const void* gate, const void* up, const void* down,
                         int64_t experts, const void* shared_gate, const void* shared_up, const void* shared_down,
                         const void* shared_gate_w, const void* tables, const void* logits, int logits_dtype,
