@@ -106,40 +106,42 @@ template <> struct RouteKey<float> {
   __device__ static __forceinline__ uint64_t wave_max(uint64_t k) { return wave_max_u64(k); }
 };
 
-// One token's top-k by selection instead of k rounds of arg-max: the k-th largest key found bit by bit from the top
-// (a candidate stays if at least k keys are at or above it: eight ballots and popcounts a bit), over the value bits
-// first and over the index bits only when the k-th value is tied past k; then the k keys at or above it, ranked
-// among themselves. Lane l holds keys i * 64 + l (i < VPL), unique, the larger chosen first (RouteKey). Leaves
-// the chosen keys in descending order in sorted[0, k) (LDS, the wave's own; scratch the same size).
+// One token's top-k by selection instead of k rounds of arg-max: the k-th largest value found bit by bit from the
+// top over the value half of the keys (a candidate stays if at least k keys are at or above it: a ballot and a
+// popcount a slot and bit); the keys above that value, and of the keys equal to it the lowest indices, as many as
+// k still wants; then the k chosen ranked among themselves. Key slot i of lane l is index i * 64 + l; keys are
+// unique, the larger chosen first (RouteKey: the value above the index's complement). Leaves the chosen keys in
+// descending order in sorted[0, k) (LDS, the wave's own; scratch the same size).
 template <typename RK, int VPL>
-__device__ __forceinline__ void wave_top_k(const typename RK::type (&key)[VPL], int K, typename RK::type* scratch,
-                                           typename RK::type* sorted) {
+__device__ __forceinline__ void select_k(const typename RK::type (&key)[VPL], int K, typename RK::type* scratch,
+                                         typename RK::type* sorted) {
   using key_t = typename RK::type;
   constexpr int BITS = 8 * (int)sizeof(key_t), IBITS = BITS / 2;  // the low half holds the index
   const int lane = threadIdx.x & 63;
+  const uint64_t below = (1ull << lane) - 1ull;
   auto count_ge = [&](key_t c) {
     int n = 0;
 #pragma unroll
     for (int i = 0; i < VPL; ++i) n += __popcll(__ballot(key[i] >= c));
     return n;
   };
-  key_t prefix = 0;
+  key_t lo = 0;  // the k-th largest value, its index half zero
   for (int bit = BITS - 1; bit >= IBITS; --bit) {
-    const key_t cand = prefix | ((key_t)1 << bit);
-    if (count_ge(cand) >= K) prefix = cand;
+    const key_t cand = lo | ((key_t)1 << bit);
+    if (count_ge(cand) >= K) lo = cand;
   }
-  if (count_ge(prefix) != K) {  // the k-th value is tied past k: the lower indices first
-    for (int bit = IBITS - 1; bit >= 0; --bit) {
-      const key_t cand = prefix | ((key_t)1 << bit);
-      if (count_ge(cand) >= K) prefix = cand;
-    }
-  }
+  const key_t hi = lo + ((key_t)1 << IBITS);  // keys at or above: a larger value (hi wraps to 0 only for the
+  int need = K - (hi ? count_ge(hi) : 0);     // largest value, which nothing exceeds)
   int base = 0;
 #pragma unroll
-  for (int i = 0; i < VPL; ++i) {
-    const bool sel = key[i] >= prefix;
+  for (int i = 0; i < VPL; ++i) {  // index order: slot i, then lane
+    const bool above = hi && key[i] >= hi;
+    const bool equal = key[i] >= lo && !above;
+    const uint64_t me = __ballot(equal);
+    const bool sel = above || (equal && __popcll(me & below) < need);
+    need -= min(need, __popcll(me));
     const uint64_t m = __ballot(sel);
-    if (sel) scratch[base + __popcll(m & ((1ull << lane) - 1ull))] = key[i];
+    if (sel) scratch[base + __popcll(m & below)] = key[i];
     base += __popcll(m);
   }
   __builtin_amdgcn_wave_barrier();
@@ -150,6 +152,47 @@ __device__ __forceinline__ void wave_top_k(const typename RK::type (&key)[VPL], 
     sorted[rank] = mine;
   }
   __builtin_amdgcn_wave_barrier();
+}
+
+// select_k over the wave's VPL keys a lane, narrowed first: the k-th largest value among the lanes' maxima bounds
+// the k-th largest key from below (those k maxima are k keys at or above it), so only the keys at or above that
+// value can be chosen; when at most 64 are, they go one a lane (in index order) and select_k runs on one slot.
+// cand: LDS, 64 keys, the wave's own.
+template <typename RK, int VPL>
+__device__ __forceinline__ void wave_top_k(const typename RK::type (&key)[VPL], int K, typename RK::type* cand,
+                                           typename RK::type* scratch, typename RK::type* sorted) {
+  using key_t = typename RK::type;
+  constexpr int BITS = 8 * (int)sizeof(key_t), IBITS = BITS / 2;
+  const int lane = threadIdx.x & 63;
+  const uint64_t below = (1ull << lane) - 1ull;
+  key_t mx = key[0];
+#pragma unroll
+  for (int i = 1; i < VPL; ++i) mx = key[i] > mx ? key[i] : mx;
+  key_t lo = 0;
+  for (int bit = BITS - 1; bit >= IBITS; --bit) {
+    const key_t c = lo | ((key_t)1 << bit);
+    if (__popcll(__ballot(mx >= c)) >= K) lo = c;
+  }
+  int n = 0;
+  uint64_t sel[VPL];
+#pragma unroll
+  for (int i = 0; i < VPL; ++i) {
+    sel[i] = __ballot(key[i] >= lo);
+    n += __popcll(sel[i]);
+  }
+  if (n > 64) {  // many keys tied at the bound: the whole set
+    select_k<RK, VPL>(key, K, scratch, sorted);
+    return;
+  }
+  int base = 0;
+#pragma unroll
+  for (int i = 0; i < VPL; ++i) {
+    if (key[i] >= lo) cand[base + __popcll(sel[i] & below)] = key[i];
+    base += __popcll(sel[i]);
+  }
+  __builtin_amdgcn_wave_barrier();
+  const key_t one[1] = {lane < n ? cand[lane] : (key_t)0};  // key 0 is no real key and is never chosen (n >= k)
+  select_k<RK, 1>(one, K, scratch, sorted);
 }
 
 template <int KIND, typename XT, typename LT, int VPL>
@@ -441,6 +484,7 @@ __global__ __launch_bounds__(FRONT_WAVES * 64) void k_moe_front(
   __shared__ int s_groups;
   __shared__ int s_wp[FRONT_WAVES][16];
   __shared__ key_t s_tk[FRONT_WAVES][2][16];
+  __shared__ key_t s_cand[FRONT_WAVES][64];
   __shared__ float s_ev[FRONT_WAVES][16];
 
   // the IQ3_S table first: it does not wait on the choice (2048 chunks, four a thread)
@@ -470,7 +514,7 @@ __global__ __launch_bounds__(FRONT_WAVES * 64) void k_moe_front(
     for (int u = 0; u < 2; ++u) {
       const int t = wave + FRONT_WAVES * u;
       if (t >= B) break;
-      wave_top_k<RK, VPL>(key[u], K, s_tk[wave][0], s_tk[wave][1]);
+      wave_top_k<RK, VPL>(key[u], K, s_cand[wave], s_tk[wave][0], s_tk[wave][1]);
       // the softmax of the chosen in rank order, as the reference sums it
       const key_t* sorted = s_tk[wave][1];
       const float top = RK::value(sorted[0]);

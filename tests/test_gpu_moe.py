@@ -160,3 +160,25 @@ def test_the_benchmark_shape_with_float32_logits(c3_layers, tables, dev):
     assert rel_err(out.float().cpu(), want) <= 1e-2
     for _ in range(3):  # the workspace reused: the same bits
         assert torch.equal(moe(logits.to(dev), x.to(dev)), out)
+
+
+@pytest.mark.parametrize("logit_dtype", [torch.bfloat16, torch.float32])
+def test_the_benchmark_shape_chooses_among_ties_by_index(logit_dtype, c3_layers, tables, dev):
+    """Logits on a coarse grid: the k-th value is shared by many experts, so the choice among them (the lower
+    indices first) decides which experts run; tokens 0-15, one of them with every logit equal."""
+    E, D, F, K = 512, 2048, 512, 10
+    fetch, lin, shared = c3_layers[("Q2_0", "Q2_0")]
+    rng = np.random.default_rng(11)
+    x = torch.from_numpy(rng.standard_normal((16, D)).astype(np.float32)).to(torch.bfloat16)
+    logits = torch.from_numpy(np.round(rng.standard_normal((16, E)) * 2).astype(np.float32) / 2).to(logit_dtype)
+    logits[3] = 0.25  # all tied: experts 0..9
+    wg = torch.from_numpy(rng.standard_normal(D).astype(np.float32) * 0.05).to(torch.bfloat16)
+    moe = SF.MoEDecode(lin["gate"], lin["up"], lin["down"], lin["sgate"], lin["sup"], lin["sdown"], wg.to(dev), K)
+    out, idx, wt = moe(logits.to(dev), x.to(dev), want_choice=True)
+    want, want_idx, want_w = OM.moe_decode_blocks(logits.float().numpy(), x.float().numpy(), K, fetch,
+                                                  ("Q2_0", "Q2_0"), (E, D, F), shared, wg.float().numpy(), tables,
+                                                  "bfloat16")
+    np.testing.assert_array_equal(idx[3].cpu().numpy(), np.arange(K))
+    np.testing.assert_array_equal(idx.cpu().numpy(), want_idx)
+    np.testing.assert_allclose(wt.cpu().numpy(), want_w, rtol=2e-6, atol=1e-7)
+    assert rel_err(out.float().cpu(), want) <= 1e-2
