@@ -408,15 +408,20 @@ constexpr int FRONT_WAVES = 8;
 // (a token chooses an expert at most once), or every token's shared pair P + t for the shared expert (e == E)
 __device__ __forceinline__ int group_pairs(int e, int E, const int* s_idx, int B, int K, int* wp) {
   const int lane = threadIdx.x & 63;
-  int n;
-  if (e < E) {
-    int jh = -1;
-    if (lane < B)
-      for (int j = 0; j < K; ++j)
-        if (s_idx[lane * K + j] == e) jh = j;
-    const uint64_t bal = __ballot(jh >= 0);
-    n = __popcll(bal);
-    if (jh >= 0) wp[__popcll(bal & ((1ull << lane) - 1ull))] = lane * K + jh;
+  int n = 0;
+  if (e < E) {  // the pairs in order (so by token): a lane a pair, three reads at once
+    int hit[(MOE_MAX_PAIRS + 63) / 64];
+#pragma unroll
+    for (int c = 0; c < (MOE_MAX_PAIRS + 63) / 64; ++c) {
+      const int p = c * 64 + lane;
+      hit[c] = p < B * K && s_idx[p] == e;
+    }
+#pragma unroll
+    for (int c = 0; c < (MOE_MAX_PAIRS + 63) / 64; ++c) {
+      const uint64_t m = __ballot(hit[c]);
+      if (hit[c]) wp[n + __popcll(m & ((1ull << lane) - 1ull))] = c * 64 + lane;
+      n += __popcll(m);
+    }
   } else {
     n = B;
     if (lane < B) wp[lane] = B * K + lane;
@@ -480,8 +485,6 @@ __global__ __launch_bounds__(FRONT_WAVES * 64) void k_moe_front(
   __shared__ int s_idx[MOE_MAX_PAIRS];
   __shared__ float s_wt[MOE_MAX_PAIRS];
   __shared__ uint32_t s_flag[WORDS];
-  __shared__ int s_gexp[MOE_MAX_PAIRS + 1];
-  __shared__ int s_groups;
   __shared__ int s_wp[FRONT_WAVES][16];
   __shared__ key_t s_tk[FRONT_WAVES][2][16];
   __shared__ key_t s_cand[FRONT_WAVES][64];
@@ -532,35 +535,28 @@ __global__ __launch_bounds__(FRONT_WAVES * 64) void k_moe_front(
     }
   }
   __syncthreads();
-  // 2. the groups: the chosen experts in ascending order, then the shared expert
-  if (wave == 0) {
-    uint32_t word = lane < WORDS ? s_flag[lane] : 0u;
-    const int cnt = __popc(word);
-    int incl = cnt;
+  // 2. the groups: the chosen experts in ascending order, then the shared expert. Each wave counts them from the
+  // flags itself and finds its block's group (no barrier); block 0 writes every group's expert for the tail.
+  const uint32_t word = lane < WORDS ? s_flag[lane] : 0u;
+  const int cnt = __popc(word);
+  int incl = cnt;
 #pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-      const int v = __shfl_up(incl, o);
-      if (lane >= o) incl += v;
-    }
-    const int total = __shfl(incl, 63);
-    int pos = incl - cnt;
-    while (word) {
-      s_gexp[pos++] = lane * 32 + __ffs(word) - 1;
-      word &= word - 1u;
-    }
-    if (lane == 0) {
-      s_gexp[total] = E;
-      s_groups = total + 1;
-    }
+  for (int o = 1; o < WORDS; o <<= 1) {
+    const int v = __shfl_up(incl, o);
+    if (lane >= o) incl += v;
   }
-  __syncthreads();
-  const int groups = s_groups;
+  const int total = __shfl(incl, WORDS - 1);
+  const int groups = total + 1;
   if (blockIdx.x == 0) {  // the choice, its weights and the groups' experts for the tail and the caller
     if (tid < P) {
       ws.idx[tid] = s_idx[tid];
       ws.w[tid] = s_wt[tid];
     }
-    if (tid < groups) ws.g_expert[tid] = s_gexp[tid];
+    if (wave == 0) {
+      int pos = incl - cnt;
+      for (uint32_t w = word; w; w &= w - 1u) ws.g_expert[pos++] = lane * 32 + __ffs(w) - 1;
+      if (lane == 0) ws.g_expert[total] = E;
+    }
     if (tid < D / 64) ws.cnt[tid] = 0;  // the tail's row tiles
     if (tid == 0) *ws.n_groups = groups;
   }
@@ -584,6 +580,13 @@ __global__ __launch_bounds__(FRONT_WAVES * 64) void k_moe_front(
   // 3. this block's run of the items: part of one group's
   int g0, first, last;
   if (!group_chunk<TILES>(groups, g0, first, last)) return;  // block-uniform
+  int e0 = E;  // the group's expert: the (g0 - excl)-th flag of the word holding it
+  if (g0 < total) {
+    const int at = __builtin_amdgcn_readfirstlane(__ffsll((unsigned long long)__ballot(lane < WORDS && incl > g0)) - 1);
+    uint32_t w = __builtin_amdgcn_readfirstlane((uint32_t)__shfl((int)word, at));
+    for (int k = g0 - (__shfl(incl, at) - __popc(w)); k > 0; --k) w &= w - 1u;
+    e0 = at * 32 + __ffs(w) - 1;
+  }
 
   // this thread's chunks of an item: matrix (0 gate, 1 up) and byte offset from the item's first row; the slot's
   // tail past the two matrices re-reads up's last chunk. Each wave waits on its own count of loads.
@@ -599,7 +602,6 @@ __global__ __launch_bounds__(FRONT_WAVES * 64) void k_moe_front(
     pre_off[j] = m >= 2 ? 15 * RB + 16 * (IT::CPR_SRC - 1) : row * RB + 16 * min(kk, IT::CPR_SRC - 1);
   }
   const int64_t ebytes = (int64_t)F * RB;
-  const int e0 = s_gexp[g0];
   const uint8_t* gate_e = e0 == E ? sh_gate : gate + (int64_t)e0 * ebytes;
   const uint8_t* up_e = e0 == E ? sh_up : up + (int64_t)e0 * ebytes;
   auto issue = [&](int item) {
