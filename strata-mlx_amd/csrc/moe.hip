@@ -43,8 +43,8 @@ struct MoeWs {
   float* gsh;         // [B]: the shared expert's gate logit, rounded to the activation type
   uint8_t* xp;        // [B][D]: the hidden states staged for gate/up's kind (xmv.h stage_index)
   uint8_t* h;         // [B*k + B][F]: swiglu(gate, up), staged for down's kind (natural order in the two-kernel path)
-  float* y;           // [B*k + B][D]: each pair's down outputs, rounded to the activation type (two-kernel path)
-  int32_t* cnt;       // [D / 64]: the tail's finished blocks a row tile, zero between calls
+  float* y;           // [B*k + B][D]: each pair's down outputs, rounded to the activation type (the common shape)
+  int32_t* cnt;       // [D / 64]: the tail's finished items a row tile when it combines, zero between calls
 };
 
 static inline size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
@@ -67,7 +67,7 @@ static size_t moe_carve(MoeWs* ws, uint8_t* base, int64_t B, int64_t k, int64_t 
   w.gsh = (float*)take(4 * B);
   w.xp = take((size_t)B * D * es);
   w.h = take((size_t)P * F * es);
-  w.y = (float*)take((size_t)4 * P * D);
+  w.y = (float*)take((size_t)P * D * 4);
   w.cnt = (int32_t*)take((size_t)4 * (D / 64 + 1));
   if (ws) *ws = w;
   return off;
@@ -384,25 +384,26 @@ __global__ __launch_bounds__(256) void k_moe_gate_up(const uint8_t* __restrict__
   }
 }
 
-// ---- the common shape (512 experts, d_model 2048, expert width 512): two kernels
+// ---- the common shape (512 experts, d_model 2048, expert width 512): three kernels
 //
-// front  route, gate and up with SwiGLU. A block of 8 waves routes the whole window itself (a wave a token: its
-//        top-k of the 512 logits), so no kernel boundary stands between the choice and the expert products, then
-//        streams a contiguous run of the items (group g, row tile r): 16 rows of gate and 16 of up of the group's
-//        expert. The groups are the chosen experts in ascending order, then the shared expert. Items go through an
-//        LDS ring filled by direct loads, NBUF - 1 in flight while one is multiplied; wave q multiplies the 16 rows
-//        of gate and of up over column eighth q with the group's activation fragments in registers (loaded as
-//        they are: the Q2_0 decode shifts each code down itself). The epilogue rounds gate and up to
-//        the activation type and writes swiglu(gate, up) per pair, in natural order. Block 0 also writes the
-//        choice, its weights and the group table and clears the tail's counters; block 1 the shared expert's gate
-//        logits.
-// tail   down and the combine. Its blocks stream contiguous runs of the items (group g, row tile of 128 rows of
-//        down of g's expert; a wave 16 rows, all 512 columns) through an LDS ring as the front does, writing each
-//        pair's outputs, rounded to the activation type, to the workspace; the block that completes a row tile's
-//        count of items combines the tile for every token.
+// front    route, gate and up with SwiGLU. A block of 8 waves routes the whole window itself (a wave a token: its
+//          top-k of the 512 logits), so no kernel boundary stands between the choice and the expert products, then
+//          streams a run of the items (group g, row tile r: 16 rows of gate and 16 of up of the group's expert)
+//          within one group. The groups are the chosen experts in ascending order, then the shared expert. Items
+//          go through an LDS ring filled by direct loads, NBUF - 1 in flight while one is multiplied; wave q
+//          multiplies the 16 rows of gate and of up over column eighth q with the group's activation fragments in
+//          registers (loaded as they are: the Q2_0 decode shifts each code down itself). The epilogue rounds gate
+//          and up to the activation type and writes swiglu(gate, up) per pair, in natural order. Block 0 also
+//          writes the choice, its weights and the groups' experts; block 1 the shared expert's gate logits.
+// tail     down. Its blocks stream runs of the items (group g, 64 rows of down of g's expert; wave (r, h) 16 rows
+//          over column half h) within one group through an LDS ring as the front does, writing each pair's
+//          outputs, rounded to the activation type, to the workspace.
+// combine  a thread an output (token, row): the routed outputs weighted in the reference's order, the shared
+//          expert gated.
 
 constexpr int FRONT_E = 512, FRONT_D = 2048, FRONT_F = 512;
 constexpr int FRONT_WAVES = 8;
+constexpr int TAIL_COMBINE_UPTO = 4;  // tokens up to which the tail combines in-kernel
 
 // the pairs of group expert e in token order, into this wave's wp[0, n): pair t * K + j of each token t choosing e
 // (a token chooses an expert at most once), or every token's shared pair P + t for the shared expert (e == E)
@@ -557,7 +558,7 @@ __global__ __launch_bounds__(FRONT_WAVES * 64) void k_moe_front(
       for (uint32_t w = word; w; w &= w - 1u) ws.g_expert[pos++] = lane * 32 + __ffs(w) - 1;
       if (lane == 0) ws.g_expert[total] = E;
     }
-    if (tid < D / 64) ws.cnt[tid] = 0;  // the tail's row tiles
+    if (tid < D / 64) ws.cnt[tid] = 0;  // the tail's row-tile counters
     if (tid == 0) *ws.n_groups = groups;
   }
   if (blockIdx.x == 1 % gridDim.x) {  // the shared expert's gate logit of each token, rounded to the activation type
@@ -682,6 +683,41 @@ __global__ __launch_bounds__(FRONT_WAVES * 64) void k_moe_front(
   store_h();
 }
 
+// the combine (strata_mlx/fused.py:448-462) of output (token t, row): experts in 8 rows j taking k = j, j + 8, ...,
+// each product rounded as the reference rounds it, then the shared expert gated. y(p) reads pair p's output.
+template <typename XT, typename YF>
+__device__ __forceinline__ void combine_one(int t, int row, int K, int B, const MoeWs& ws, XT* out, YF&& y) {
+#pragma clang fp contract(off)
+  constexpr int D = FRONT_D;
+  float yk[16], wk[16];  // k <= 16
+#pragma unroll
+  for (int kk = 0; kk < 16; ++kk) {
+    yk[kk] = kk < K ? y(t * K + kk) : 0.0f;
+    wk[kk] = kk < K ? ws.w[t * K + kk] : 0.0f;
+  }
+  const float ys = y(B * K + t);
+  float acc = 0.0f;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    if (j < K) {
+      float part = 0.0f;
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        const int kk = j + 8 * i;
+        if (kk < K) {
+          const float prod = yk[kk] * wk[kk];
+          part = prod + part;
+        }
+      }
+      acc = j == 0 ? part : part + acc;
+    }
+  }
+  const XT routed = from_f32<XT>(acc);
+  const XT gate = from_f32<XT>(1.0f / (1.0f + expf(-ws.gsh[t])));
+  const XT shared = from_f32<XT>(to_f32(gate) * ys);
+  out[(int64_t)t * D + row] = from_f32<XT>(to_f32(routed) + to_f32(shared));
+}
+
 // an item of the tail: 64 rows of down (wave (r, h): rows 16r.. of column half h), 16-byte chunks copied as they
 // lie (the rows of a Q2_0 / IQ3_S expert of width 512 are 144 / 220 bytes: 16 rows at that stride fall in distinct
 // or two-way shared bank windows); wave w loads the runs of 64 chunks w, w + 8, ...
@@ -704,7 +740,7 @@ template <int KIND, typename XT, int TPG>
 __global__ __launch_bounds__(FRONT_WAVES * 64) void k_moe_tail(const uint8_t* __restrict__ down,
                                                                const uint8_t* __restrict__ sh_down, int K, int B,
                                                                TailPlan tp, const uint8_t* __restrict__ signed_tab,
-                                                               MoeWs ws, XT* __restrict__ out) {
+                                                               MoeWs ws, int combine, XT* __restrict__ out) {
 #pragma clang fp contract(off)
   using MT = XT;
   using IT = TailItem<KIND>;
@@ -769,16 +805,21 @@ __global__ __launch_bounds__(FRONT_WAVES * 64) void k_moe_tail(const uint8_t* __
   x_finish<KIND, XT, TPG, GPER>(X, xraw);
 
   const DecodeRegs kr = decode_regs<KIND, MT>();
-  // each pair's outputs, rounded to the activation type, go out as device-scope stores (through the XCD's L2 to
-  // memory) at the start of the next item
-  float yv[TPG];
+  // each pair's outputs, rounded to the activation type, stored at the start of the next item; with the combine
+  // in this kernel as device-scope stores (written through the XCD's L2) for the block that combines them
+  XT yv[TPG];
   int yp[TPG], yrow = -1;
   auto store_y = [&]() {
     if (yrow >= 0) {
 #pragma unroll
-      for (int t = 0; t < TPG; ++t)
-        if (yp[t] >= 0)
-          __hip_atomic_store(&ws.y[(int64_t)yp[t] * D + yrow], yv[t], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      for (int t = 0; t < TPG; ++t) {
+        if (yp[t] < 0) continue;
+        float* at = ws.y + (int64_t)yp[t] * D + yrow;
+        if (combine)
+          __hip_atomic_store(at, to_f32(yv[t]), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        else
+          *at = to_f32(yv[t]);
+      }
     }
   };
   for (int item = first; item < last; ++item) {
@@ -805,16 +846,17 @@ __global__ __launch_bounds__(FRONT_WAVES * 64) void k_moe_tail(const uint8_t* __
 #pragma unroll
       for (int t = 0; t < TPG; ++t) {
         const int tt = q * TPG + t;
-        yv[t] = to_f32(from_f32<XT>(acc[t] + red[(rg * 64 + lane) * TPG + t]));
+        yv[t] = from_f32<XT>(acc[t] + red[(rg * 64 + lane) * TPG + t]);
         yp[t] = tt < n_tok ? s_wp[wave][tt] : -1;
       }
     }
   }
   store_y();
+  if (!combine) return;
   // Count this block's items into their row tiles' counters once every output of them is out (vmcnt 0: the
   // device-scope stores reached memory); the block that completes a tile's count combines the tile, reading the
-  // outputs with device-scope loads. No device-wide fence: its L2 write-back and invalidation serialize the
-  // blocks of an XCD.
+  // outputs with device-scope loads, and clears the counter. No device-wide fence: its L2 write-back and
+  // invalidation serialize the blocks of an XCD.
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
   if (tid < last - first) {
@@ -824,41 +866,21 @@ __global__ __launch_bounds__(FRONT_WAVES * 64) void k_moe_tail(const uint8_t* __
   }
   __syncthreads();
   const int ncomb = s_ncomb;
-  // the combine (strata_mlx/fused.py:448-462): experts in 8 rows j taking k = j, j + 8, ..., each product rounded;
-  // every (tile, token, row) of the block's tiles at once, so their loads go out together
   for (int qv = tid; qv < ncomb * B * IT::ROWS; qv += NT) {
     const int c = qv / (B * IT::ROWS), rest = qv - c * (B * IT::ROWS);
     const int t = rest / IT::ROWS, row = s_comb[c] * IT::ROWS + rest % IT::ROWS;
-    float y[16], w[16];  // k <= 16
-#pragma unroll
-    for (int kk = 0; kk < 16; ++kk) {
-      y[kk] = kk < K ? __hip_atomic_load(&ws.y[(int64_t)(t * K + kk) * D + row], __ATOMIC_RELAXED,
-                                         __HIP_MEMORY_SCOPE_AGENT) : 0.0f;
-      w[kk] = kk < K ? ws.w[t * K + kk] : 0.0f;
-    }
-    const float ys = __hip_atomic_load(&ws.y[(int64_t)(P + t) * D + row], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    float acc2 = 0.0f;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      if (j < K) {
-        float part = 0.0f;
-#pragma unroll
-        for (int i = 0; i < 2; ++i) {
-          const int kk = j + 8 * i;
-          if (kk < K) {
-            const float prod = y[kk] * w[kk];
-            part = prod + part;
-          }
-        }
-        acc2 = j == 0 ? part : part + acc2;
-      }
-    }
-    const XT routed = from_f32<XT>(acc2);
-    const XT gate = from_f32<XT>(1.0f / (1.0f + expf(-ws.gsh[t])));
-    const XT shared = from_f32<XT>(to_f32(gate) * ys);
-    out[(int64_t)t * D + row] = from_f32<XT>(to_f32(routed) + to_f32(shared));
+    combine_one<XT>(t, row, K, B, ws, out, [&](int p) {
+      return __hip_atomic_load(ws.y + (int64_t)p * D + row, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    });
   }
   if (tid < ncomb) __hip_atomic_store(&ws.cnt[s_comb[tid]], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// the combine as a kernel of its own after the tail, a thread an output
+template <typename XT>
+__global__ __launch_bounds__(256) void k_moe_combine(int K, int B, MoeWs ws, XT* __restrict__ out) {
+  const int row = blockIdx.x * 256 + threadIdx.x;
+  combine_one<XT>(blockIdx.y, row, K, B, ws, out, [&](int p) { return ws.y[(int64_t)p * FRONT_D + row]; });
 }
 
 // ---- down and the combine: a block is 16 output rows of every group's expert
@@ -1087,9 +1109,19 @@ static int launch_moe(const uint8_t* gate, const uint8_t* up, const uint8_t* dow
     const int64_t grid = std::min<int64_t>(most, (int64_t)device_cus() * per_cu);
     if (grid < std::min<int64_t>(B * K, E) + 1)  // a block at least for each group (a block's items are then at
       return fail(E_UNSUPPORTED, "moe_decode: %lld blocks for the tail", (long long)grid);  // most TILES)
-    hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(nt), lds, stream, down, sd, (int)K, (int)B, tp, stab, ws, out);
+    // a few tokens: the tail's last block of a row tile combines it (no third launch); more: a combine kernel
+    // (the tiles' last blocks would each combine several tiles, serially)
+    const int combine = B <= TAIL_COMBINE_UPTO;
+    hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(nt), lds, stream, down, sd, (int)K, (int)B, tp, stab, ws,
+                       combine, out);
     st = check_launch("moe_decode tail");
     if (st) return st;
+    if (!combine) {
+      hipLaunchKernelGGL(k_moe_combine<XT>, dim3((unsigned)(FRONT_D / 256), (unsigned)B), dim3(256), 0, stream,
+                         (int)K, (int)B, ws, out);
+      st = check_launch("moe_decode combine");
+      if (st) return st;
+    }
   }
   if (phases & 1) {
     auto route = [&](auto vc) {
