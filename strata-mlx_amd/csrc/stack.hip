@@ -40,7 +40,9 @@ __global__ __launch_bounds__(NWMAX * 64) void k_stack_mv(const uint8_t* __restri
   extern __shared__ u32x4 dyn[];
   uint8_t* lds = (uint8_t*)dyn;
   const uint32_t lds_base = SH_LDS_ADDR(dyn);
-  float* red = (float*)(lds + P.red_off);  // [kw - 1][rg][64][TPG]: the column splits' partial sums
+  // [2][kw - 1][rg][64][TPG]: the column splits' partial sums of the last two items (read a barrier later)
+  float* red = (float*)(lds + P.red_off);
+  const int red_sz = (P.kw - 1) * P.rg * 64 * TPG;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int rg = wave % P.rg, kh = wave / P.rg;
@@ -92,17 +94,23 @@ __global__ __launch_bounds__(NWMAX * 64) void k_stack_mv(const uint8_t* __restri
 
   const DecodeRegs kr = decode_regs<KIND, MT>();
   XRegs<KIND, TPG, GPER> X;
-  // an item's results are stored at the start of the next item, before its loads are issued: a store counts on
-  // vmcnt like a load, and issued after an item's loads it would make the wait for the item before them wait for
-  // part of them too
-  float total[TPG];
-  int64_t out_at = -1;  // the element of the last item's results for this lane's first token, or -1: none
-  auto store_out = [&]() {
-    if (out_at >= 0) {
+  // An item's results are reduced and stored at the start of the next item, after its barrier (which also makes the
+  // other column splits' partial sums visible: one barrier an item) and before its loads are issued (a store counts
+  // on vmcnt like a load: issued after an item's loads, the wait for the item before them would wait for part of
+  // them too).
+  float pend[TPG];
+  int64_t pend_at = -1;  // the element of the last item's results for this lane's first token, or -1: none
+  int pend_buf = 0;
+  auto finish = [&]() {
+    if (pend_at >= 0) {
+      const float* rb = red + pend_buf * red_sz;
       const int g = lane >> 4;
 #pragma unroll
-      for (int t = 0; t < TPG; ++t)
-        if (g * TPG + t < P.tokens) out[out_at + (int64_t)t * P.rows] = from_f32<XT>(total[t]);
+      for (int t = 0; t < TPG; ++t) {
+        float total = pend[t];
+        for (int k2 = 1; k2 < P.kw; ++k2) total += rb[(((k2 - 1) * P.rg + rg) * 64 + lane) * TPG + t];
+        if (g * TPG + t < P.tokens) out[pend_at + (int64_t)t * P.rows] = from_f32<XT>(total);
+      }
     }
   };
   int m = -1;
@@ -110,7 +118,7 @@ __global__ __launch_bounds__(NWMAX * 64) void k_stack_mv(const uint8_t* __restri
     const int ahead = min(P.nbuf - 2, last - 1 - item);  // items issued after this one
     wait_vmcnt(ahead * P.loads);
     lds_sync();  // this item is in LDS for every wave; every wave is done with the item before
-    store_out();
+    finish();
     if (item + P.nbuf - 1 < last) issue(item + P.nbuf - 1);
     const int mi = item / P.items_per_mat;
     if (mi != m) {  // a new matrix: this wave's activation fragments and offset sums
@@ -130,25 +138,21 @@ __global__ __launch_bounds__(NWMAX * 64) void k_stack_mv(const uint8_t* __restri
       item_mac<KIND, MT, TPG, GPER>(row0 + (size_t)rg * 16 * P.rstride + wcol, P.rstride, X, (const uint32_t*)lds,
                                     kr, acc);
     }
-    if (P.kw > 1) {
-      if (kh > 0) {
+    if (kh > 0) {
 #pragma unroll
-        for (int t = 0; t < TPG; ++t) red[(((kh - 1) * P.rg + rg) * 64 + lane) * TPG + t] = acc[t];
-      }
-      lds_sync();
+      for (int t = 0; t < TPG; ++t) red[(item & 1) * red_sz + (((kh - 1) * P.rg + rg) * 64 + lane) * TPG + t] = acc[t];
     }
-    out_at = -1;
+    pend_at = -1;
     const int row = r0 + rg * 16 + (lane & 15);
     if (kh == 0 && rg * 16 < rows_here && row < P.rows) {
 #pragma unroll
-      for (int t = 0; t < TPG; ++t) {
-        total[t] = acc[t];
-        for (int k2 = 1; k2 < P.kw; ++k2) total[t] += red[(((k2 - 1) * P.rg + rg) * 64 + lane) * TPG + t];
-      }
-      out_at = ((int64_t)m * P.tokens + (lane >> 4) * TPG) * P.rows + row;
+      for (int t = 0; t < TPG; ++t) pend[t] = acc[t];
+      pend_at = ((int64_t)m * P.tokens + (lane >> 4) * TPG) * P.rows + row;
+      pend_buf = item & 1;
     }
   }
-  store_out();
+  lds_sync();
+  finish();
   wait_vmcnt(0);
 }
 
@@ -175,16 +179,22 @@ static int launch_stack(const uint8_t* blocks, const uint8_t* tables, int64_t n_
     return fail(E_UNSUPPORTED, "stack_matvec: rows of %lld bytes", (long long)P.rbytes);
   P.buf_bytes = P.loads * 16 * nt;
   P.ring_off = KIND == IQ3_S ? IQ3S_SIGNED_BYTES : 0;
-  const size_t red = (size_t)(P.kw - 1) * P.rg * 64 * TPG * 4, tail = 128;
+  const size_t red = (size_t)2 * (P.kw - 1) * P.rg * 64 * TPG * 4, tail = 128;
   const size_t cap = 160 * 1024;
   // direct loads into LDS land below 128 KiB: the table and the ring stay under it
   const size_t dma_limit = 128 * 1024;
-  P.nbuf = 3;
-  while (P.nbuf > 2 && ((size_t)P.ring_off + (size_t)P.nbuf * P.buf_bytes + red + tail > cap ||
-                        (size_t)P.ring_off + (size_t)P.nbuf * P.buf_bytes > dma_limit))
-    --P.nbuf;
-  if ((size_t)P.ring_off + (size_t)P.nbuf * P.buf_bytes > dma_limit)
-    return fail(E_UNSUPPORTED, "stack_matvec: a ring of %d x %d bytes past the 128 KiB direct-load range", P.nbuf,
+  // the deepest ring (up to six items) that leaves room for two blocks a CU, else the deepest for one
+  auto fits = [&](int nb, size_t limit) {
+    return (size_t)P.ring_off + (size_t)nb * P.buf_bytes + red + tail <= limit &&
+           (size_t)P.ring_off + (size_t)nb * P.buf_bytes <= dma_limit;
+  };
+  P.nbuf = 0;
+  for (int nb = 6; nb >= 3 && !P.nbuf; --nb)
+    if (fits(nb, cap / 2)) P.nbuf = nb;
+  for (int nb = 6; nb >= 2 && !P.nbuf; --nb)
+    if (fits(nb, cap)) P.nbuf = nb;
+  if (!P.nbuf)
+    return fail(E_UNSUPPORTED, "stack_matvec: no ring of %d-byte items fits in LDS below the 128 KiB direct-load range",
                 P.buf_bytes);
   P.red_off = P.ring_off + P.nbuf * P.buf_bytes;
   const size_t lds = (size_t)P.red_off + red + tail;
