@@ -165,7 +165,7 @@ static int launch_stack(const uint8_t* blocks, const uint8_t* tables, int64_t n_
   P.tokens = (int)tokens;
   P.ngroups = (int)(cols / scale_group<KIND>());
   P.kw = P.ngroups / GPER;
-  P.rg = few ? 1 : std::max(1, 8 / P.kw);
+  P.rg = few ? 1 : std::max(1, (KIND == Q2_0 ? 8 : 16) / P.kw);  // 8 (Q2_0) or 16 (IQ3_S) waves a block
   P.nw = P.rg * P.kw;
   const int IR = 16 * P.rg, nt = 64 * P.nw;
   P.rbytes = row_bytes(KIND, cols);
@@ -238,13 +238,15 @@ int sh_stack_matvec(int kind, const void* blocks, const void* tables, int64_t n_
     return fail(E_ARG, "stack_matvec: activations and tables must be 16-byte aligned");
   // a wave's columns: GPER scale groups (8 or 4 Q2_0 blocks, 16 or 8 IQ3_S runs), at most 16 waves across a row
   const int64_t ngroups = cols / (kind == Q2_0 ? 64 : 32);
-  const int gper = kind == Q2_0 ? (ngroups % 8 == 0 ? 8 : 4) : (ngroups % 16 == 0 ? 16 : 8);
+  // Q2_0: eight groups a wave (its decode is a few VALU ops a weight: fewer, wider waves); IQ3_S: as few as a row
+  // of at most 16 waves allows (its table lookups want more waves a SIMD to hide them)
+  const int gper = kind == Q2_0 ? (ngroups % 8 == 0 ? 8 : 4) : (ngroups % 8 == 0 && ngroups / 8 <= 16 ? 8 : 16);
   if (ngroups / gper > 16)
     return fail(E_UNSUPPORTED, "stack_matvec: %lld columns (at most %d)", (long long)cols,
                 16 * gper * (kind == Q2_0 ? 64 : 32));
   const int tpg = tokens <= 4 ? 1 : tokens <= 8 ? 2 : 4;
   // few items to go round the CUs: one row group a block, one item a block
-  const int64_t kw = ngroups / gper, ir = 16 * std::max<int64_t>(1, 8 / kw);
+  const int64_t kw = ngroups / gper, ir = 16 * std::max<int64_t>(1, (kind == Q2_0 ? 8 : 16) / kw);
   const bool few = n_mats * ((rows + ir - 1) / ir) < 2 * (int64_t)device_cus();
   return with_half_dtype(x_dtype, [&](auto* tp) {
     using XT = std::remove_pointer_t<decltype(tp)>;
