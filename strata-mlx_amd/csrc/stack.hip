@@ -21,7 +21,7 @@
 
 namespace sh {
 
-constexpr int STACK_LMAX = 16;  // direct loads a thread an item, at most
+constexpr int STACK_LMAX = 6;  // direct loads a thread an item, at most
 
 // one launch's shape, shared by host and device through the kernel arguments
 struct StackPlan {
@@ -32,7 +32,7 @@ struct StackPlan {
   int ring_off, buf_bytes, red_off;                        // LDS byte offsets and sizes
 };
 
-template <int KIND, typename XT, int TPG, int GPER, int NWMAX>
+template <int KIND, typename XT, int TPG, int GPER, int NWMAX, int RW>
 __global__ __launch_bounds__(NWMAX * 64) void k_stack_mv(const uint8_t* __restrict__ blocks, StackPlan P,
                                                         const XT* __restrict__ x, XT* __restrict__ out,
                                                         const uint8_t* __restrict__ signed_tab) {
@@ -45,7 +45,9 @@ __global__ __launch_bounds__(NWMAX * 64) void k_stack_mv(const uint8_t* __restri
   const int red_sz = (P.kw - 1) * P.rg * 64 * TPG;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int rg = wave % P.rg, kh = wave / P.rg;
+  // RW 1: wave (r, h) multiplies row group r over column split h; RW 2: wave h both row groups over split h (one
+  // set of activation registers for two row groups: fewer registers a row, more waves a SIMD)
+  const int rg0 = RW == 1 ? wave % P.rg : 0, kh = RW == 1 ? wave / P.rg : wave;
   const int nt = 64 * P.nw, IR = 16 * P.rg;
   const int wcol = KIND == Q2_0 ? kh * GPER * 18 : (kh * GPER / 8) * 110;  // the wave's first group in a row
 
@@ -98,18 +100,22 @@ __global__ __launch_bounds__(NWMAX * 64) void k_stack_mv(const uint8_t* __restri
   // other column splits' partial sums visible: one barrier an item) and before its loads are issued (a store counts
   // on vmcnt like a load: issued after an item's loads, the wait for the item before them would wait for part of
   // them too).
-  float pend[TPG];
-  int64_t pend_at = -1;  // the element of the last item's results for this lane's first token, or -1: none
+  float pend[RW][TPG];
+  int64_t pend_at[RW];  // the element of the last item's results for this lane's first token, or -1: none
+#pragma unroll
+  for (int r = 0; r < RW; ++r) pend_at[r] = -1;
   int pend_buf = 0;
   auto finish = [&]() {
-    if (pend_at >= 0) {
-      const float* rb = red + pend_buf * red_sz;
-      const int g = lane >> 4;
+    const float* rb = red + pend_buf * red_sz;
+    const int g = lane >> 4;
+#pragma unroll
+    for (int r = 0; r < RW; ++r) {
+      if (pend_at[r] < 0) continue;
 #pragma unroll
       for (int t = 0; t < TPG; ++t) {
-        float total = pend[t];
-        for (int k2 = 1; k2 < P.kw; ++k2) total += rb[(((k2 - 1) * P.rg + rg) * 64 + lane) * TPG + t];
-        if (g * TPG + t < P.tokens) out[pend_at + (int64_t)t * P.rows] = from_f32<XT>(total);
+        float total = pend[r][t];
+        for (int k2 = 1; k2 < P.kw; ++k2) total += rb[(((k2 - 1) * P.rg + rg0 + r) * 64 + lane) * TPG + t];
+        if (g * TPG + t < P.tokens) out[pend_at[r] + (int64_t)t * P.rows] = from_f32<XT>(total);
       }
     }
   };
@@ -127,36 +133,45 @@ __global__ __launch_bounds__(NWMAX * 64) void k_stack_mv(const uint8_t* __restri
     }
     const int r0 = (item - m * P.items_per_mat) * IR;
     const int rows_here = min(IR, P.rows - r0);
-    float acc[TPG];
+    float acc[RW][TPG];
 #pragma unroll
-    for (int t = 0; t < TPG; ++t) acc[t] = 0.0f;
+    for (int r = 0; r < RW; ++r)
+#pragma unroll
+      for (int t = 0; t < TPG; ++t) acc[r][t] = 0.0f;
     const uint8_t* row0 = lds + P.ring_off + (item % P.nbuf) * P.buf_bytes + (P.padded ? 0 : lead_of(src_of(item)));
-    if (rg * 16 < rows_here) {
-      // nothing of the LDS / scalar-load counter pending (scalar loads return out of order: with one pending the
-      // multiply's reads could only be waited for all at once)
-      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-      item_mac<KIND, MT, TPG, GPER>(row0 + (size_t)rg * 16 * P.rstride + wcol, P.rstride, X, (const uint32_t*)lds,
-                                    kr, acc);
-    }
+    // nothing of the LDS / scalar-load counter pending (scalar loads return out of order: with one pending the
+    // multiply's reads could only be waited for all at once)
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+    for (int r = 0; r < RW; ++r)
+      if ((rg0 + r) * 16 < rows_here)
+        item_mac<KIND, MT, TPG, GPER>(row0 + (size_t)(rg0 + r) * 16 * P.rstride + wcol, P.rstride, X,
+                                      (const uint32_t*)lds, kr, acc[r]);
     if (kh > 0) {
 #pragma unroll
-      for (int t = 0; t < TPG; ++t) red[(item & 1) * red_sz + (((kh - 1) * P.rg + rg) * 64 + lane) * TPG + t] = acc[t];
-    }
-    pend_at = -1;
-    const int row = r0 + rg * 16 + (lane & 15);
-    if (kh == 0 && rg * 16 < rows_here && row < P.rows) {
+      for (int r = 0; r < RW; ++r)
 #pragma unroll
-      for (int t = 0; t < TPG; ++t) pend[t] = acc[t];
-      pend_at = ((int64_t)m * P.tokens + (lane >> 4) * TPG) * P.rows + row;
-      pend_buf = item & 1;
+        for (int t = 0; t < TPG; ++t)
+          red[(item & 1) * red_sz + (((kh - 1) * P.rg + rg0 + r) * 64 + lane) * TPG + t] = acc[r][t];
     }
+#pragma unroll
+    for (int r = 0; r < RW; ++r) {
+      pend_at[r] = -1;
+      const int row = r0 + (rg0 + r) * 16 + (lane & 15);
+      if (kh == 0 && (rg0 + r) * 16 < rows_here && row < P.rows) {
+#pragma unroll
+        for (int t = 0; t < TPG; ++t) pend[r][t] = acc[r][t];
+        pend_at[r] = ((int64_t)m * P.tokens + (lane >> 4) * TPG) * P.rows + row;
+      }
+    }
+    pend_buf = item & 1;
   }
   lds_sync();
   finish();
   wait_vmcnt(0);
 }
 
-template <int KIND, typename XT, int TPG, int GPER>
+template <int KIND, typename XT, int TPG, int GPER, int RW>
 static int launch_stack(const uint8_t* blocks, const uint8_t* tables, int64_t n_mats, int64_t rows, int64_t cols,
                         const XT* x, int64_t tokens, XT* out, bool few, hipStream_t stream) {
   StackPlan P;
@@ -165,8 +180,8 @@ static int launch_stack(const uint8_t* blocks, const uint8_t* tables, int64_t n_
   P.tokens = (int)tokens;
   P.ngroups = (int)(cols / scale_group<KIND>());
   P.kw = P.ngroups / GPER;
-  P.rg = few ? 1 : std::max(1, (KIND == Q2_0 ? 8 : 16) / P.kw);  // 8 (Q2_0) or 16 (IQ3_S) waves a block
-  P.nw = P.rg * P.kw;
+  P.rg = RW == 2 ? 2 : few ? 1 : std::max(1, (KIND == Q2_0 ? 8 : 16) / P.kw);
+  P.nw = RW == 2 ? P.kw : P.rg * P.kw;
   const int IR = 16 * P.rg, nt = 64 * P.nw;
   P.rbytes = row_bytes(KIND, cols);
   P.mat_bytes = rows * P.rbytes;
@@ -207,7 +222,7 @@ static int launch_stack(const uint8_t* blocks, const uint8_t* tables, int64_t n_
                        tables ? tables + TAB_IQ3S_SIGNED : nullptr);
     return check_launch("stack_matvec");
   };
-  return P.nw <= 8 ? run(k_stack_mv<KIND, XT, TPG, GPER, 8>) : run(k_stack_mv<KIND, XT, TPG, GPER, 16>);
+  return P.nw <= 8 ? run(k_stack_mv<KIND, XT, TPG, GPER, 8, RW>) : run(k_stack_mv<KIND, XT, TPG, GPER, 16, RW>);
 }
 
 }  // namespace sh
@@ -238,22 +253,31 @@ int sh_stack_matvec(int kind, const void* blocks, const void* tables, int64_t n_
     return fail(E_ARG, "stack_matvec: activations and tables must be 16-byte aligned");
   // a wave's columns: GPER scale groups (8 or 4 Q2_0 blocks, 16 or 8 IQ3_S runs), at most 16 waves across a row
   const int64_t ngroups = cols / (kind == Q2_0 ? 64 : 32);
-  // Q2_0: eight groups a wave (its decode is a few VALU ops a weight: fewer, wider waves); IQ3_S: as few as a row
-  // of at most 16 waves allows (its table lookups want more waves a SIMD to hide them)
-  const int gper = kind == Q2_0 ? (ngroups % 8 == 0 ? 8 : 4) : (ngroups % 8 == 0 && ngroups / 8 <= 16 ? 8 : 16);
-  if (ngroups / gper > 16)
+  // Streaming Q2_0 for up to 4 tokens: 8 column splits of 4 groups, each wave both row groups of a 32-row item (one
+  // set of activation registers: two blocks a CU), when that covers a row in at most 8 waves. Otherwise a wave a
+  // row group: Q2_0 8 (else 4) groups a wave in 8-wave blocks; IQ3_S 8 (else 16) groups a wave in blocks of up to
+  // 16 waves (its table lookups want more waves a SIMD). Measured on the 3072 x 2048 stream.
+  const int64_t small = 4;
+  const bool rw2_shape = kind == Q2_0 && tokens <= 4 && ngroups % small == 0 && ngroups / small <= 8;
+  const int gper1 = kind == Q2_0 ? (ngroups % 8 == 0 ? 8 : 4) : (ngroups % 8 == 0 && ngroups / 8 <= 16 ? 8 : 16);
+  if (ngroups / gper1 > 16)
     return fail(E_UNSUPPORTED, "stack_matvec: %lld columns (at most %d)", (long long)cols,
-                16 * gper * (kind == Q2_0 ? 64 : 32));
+                16 * gper1 * (kind == Q2_0 ? 64 : 32));
   const int tpg = tokens <= 4 ? 1 : tokens <= 8 ? 2 : 4;
   // few items to go round the CUs: one row group a block, one item a block
-  const int64_t kw = ngroups / gper, ir = 16 * std::max<int64_t>(1, (kind == Q2_0 ? 8 : 16) / kw);
+  const int64_t kw1 = ngroups / gper1, ir = rw2_shape ? 32 : 16 * std::max<int64_t>(1, (kind == Q2_0 ? 8 : 16) / kw1);
   const bool few = n_mats * ((rows + ir - 1) / ir) < 2 * (int64_t)device_cus();
+  const bool rw2 = rw2_shape && !few;
+  const int gper = rw2 ? (int)small : gper1;
   return with_half_dtype(x_dtype, [&](auto* tp) {
     using XT = std::remove_pointer_t<decltype(tp)>;
     auto go = [&](auto kc, auto gc, auto tc) {
       constexpr int K = decltype(kc)::value, G = decltype(gc)::value, T = decltype(tc)::value;
-      return launch_stack<K, XT, T, G>((const uint8_t*)blocks, (const uint8_t*)tables, n_mats, rows, cols,
-                                       (const XT*)x, tokens, (XT*)out, few, (hipStream_t)stream);
+      if (rw2)
+        return launch_stack<K, XT, T, G, 2>((const uint8_t*)blocks, (const uint8_t*)tables, n_mats, rows, cols,
+                                            (const XT*)x, tokens, (XT*)out, few, (hipStream_t)stream);
+      return launch_stack<K, XT, T, G, 1>((const uint8_t*)blocks, (const uint8_t*)tables, n_mats, rows, cols,
+                                          (const XT*)x, tokens, (XT*)out, few, (hipStream_t)stream);
     };
     auto by_t = [&](auto kc, auto gc) {
       return tpg == 1 ? go(kc, gc, kind_c<1>{}) : tpg == 2 ? go(kc, gc, kind_c<2>{}) : go(kc, gc, kind_c<4>{});
