@@ -29,7 +29,8 @@ struct AttnArgs {
   const void* v;
   const int32_t* table;      // paged: physical page of each tile of 16 positions; cells: (n_q, ctx) cell ids
   const uint8_t* real;       // cells: (n_q, ctx) validity; paged: null
-  float* ws;                 // [splits][units][rows][D + 2]: max, sum, output
+  float* ws;                 // the workspace: wm, wl [splits][units][rows] max and sum; wo the outputs, as the
+  float *wm, *wl, *wo;       // lanes hold them: [splits][units][zgroups][4 row tiles][D / 16][64 lanes][4 rows]
   void* out;                 // (n_q, hq, D)
   int n_q, hq, hkv, ctx;     // ctx: paged context length, or cells a query
   int64_t kv_len;            // cells: rows of one KV head; paged: pages in the pool
@@ -203,15 +204,15 @@ __global__ __launch_bounds__(ATT_NT) void k_attn_split(AttnArgs a) {
   }
 
   // ---- merge the PL phases of each row tile in LDS, then the first phase's wave writes the split's partial
-  float* red = (float*)dyn;  // [ph][rt][64 lanes]: m, l, then O [ph][rt][dims][16 rows]
-  float* redo = red + 2 * ATT_WAVES * 64;
+  // [ph][rt][64 lanes]: m, l; then O as [ph][rt][dim tile][64 lanes] of the lanes' four accumulators (16-byte
+  // stores and loads, consecutive across lanes: no bank conflicts)
+  float* red = (float*)dyn;
+  f32x4* redo = (f32x4*)(red + 2 * ATT_WAVES * 64);
   if (PL > 1) {
     red[(ph * RT4 + rt) * 64 + lane] = m_run;
     red[ATT_WAVES * 64 + (ph * RT4 + rt) * 64 + lane] = l_run;
 #pragma unroll
-    for (int dt = 0; dt < NDT; ++dt)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) redo[((ph * RT4 + rt) * D + 16 * dt + n) * 16 + 4 * g + i] = O[dt][i];
+    for (int dt = 0; dt < NDT; ++dt) redo[((ph * RT4 + rt) * NDT + dt) * 64 + lane] = O[dt];
     lds_sync();
     if (ph == 0) {
       // lane (g, n): its column row n for m, l; O rows 4g + i
@@ -226,82 +227,81 @@ __global__ __launch_bounds__(ATT_NT) void k_attn_split(AttnArgs a) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) fr[p2][i] = exp2f(red[(p2 * RT4 + rt) * 64 + 4 * g + i] - __shfl(base, 4 * g + i));
 #pragma unroll
-      for (int dt = 0; dt < NDT; ++dt)
+      for (int dt = 0; dt < NDT; ++dt) {
+        f32x4 o = {0.0f, 0.0f, 0.0f, 0.0f};
+        for (int p2 = 0; p2 < PL; ++p2) {
+          const f32x4 v = redo[((p2 * RT4 + rt) * NDT + dt) * 64 + lane];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          float o = 0.0f;
-          for (int p2 = 0; p2 < PL; ++p2) o += redo[((p2 * RT4 + rt) * D + 16 * dt + n) * 16 + 4 * g + i] * fr[p2][i];
-          O[dt][i] = o;
+          for (int i = 0; i < 4; ++i) o[i] += v[i] * fr[p2][i];
         }
+        O[dt] = o;
+      }
       m_run = m_all;
       l_run = l_all;
     }
   }
   if (ph == 0 && rt < RT) {
-    float* w = a.ws + ((int64_t)split * a.units + unit) * (int64_t)a.rows * (D + 2);
-    const int r_col = zrow + r_local;  // lane's column row (m, l)
-    if (g == 0 && r_local < rows_here) {
-      w[(int64_t)r_col * (D + 2)] = m_run;
-      w[(int64_t)r_col * (D + 2) + 1] = l_run;
+    const int64_t su = (int64_t)split * a.units + unit;
+    if (g == 0 && r_local < rows_here) {  // lane's column row: max and sum
+      a.wm[su * a.rows + zrow + r_local] = m_run;
+      a.wl[su * a.rows + zrow + r_local] = l_run;
     }
+    // the outputs as the lanes hold them (rows 4g + i of the row tile, dim 16 dt + n): a 16-byte store a dim tile
+    f32x4* wo = (f32x4*)a.wo + ((su * gridDim.z + blockIdx.z) * 4 + rt) * NDT * 64;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int rl = 16 * rt + 4 * g + i;
-      if (rl < rows_here) {
-#pragma unroll
-        for (int dt = 0; dt < NDT; ++dt) w[(int64_t)(zrow + rl) * (D + 2) + 2 + 16 * dt + n] = O[dt][i];
-      }
-    }
+    for (int dt = 0; dt < NDT; ++dt) wo[dt * 64 + lane] = O[dt];
   }
 }
 
-// merge the splits of one (unit, row): out = sum_s O_s 2^(m_s - m) / sum_s l_s 2^(m_s - m); a row that sees no
-// position (every cell masked) gives zeros. The splits' factors are worked out once into LDS by the block's
-// threads together; then thread d sums dimension d over the splits.
+// merge the splits of 16 rows x 16 dims (block (dim tile, row tile, unit x row group)):
+// out = sum_s O_s 2^(m_s - m) / sum_s l_s 2^(m_s - m); a row that sees no position (every cell masked) gives zeros.
+// The 16 rows' factors of every split go to LDS first (16 threads a row); then thread t sums element t of the
+// tile's lane layout over the splits (256 consecutive floats a split: one coalesced read).
 constexpr int ATT_MAX_SPLITS = 1024;
-
-__device__ __forceinline__ float block_reduce(float v, bool is_max, float* scratch) {
-  for (int o = 32; o > 0; o >>= 1) {
-    const float w = __shfl_xor(v, o);
-    v = is_max ? fmaxf(v, w) : v + w;
-  }
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
-  __syncthreads();
-  if (lane == 0) scratch[wave] = v;
-  __syncthreads();
-  v = scratch[0];
-  for (int i = 1; i < nw; ++i) v = is_max ? fmaxf(v, scratch[i]) : v + scratch[i];
-  return v;
-}
 
 template <typename XT, int D, bool CELLS>
 __global__ __launch_bounds__(256) void k_attn_merge(AttnArgs a) {
-  __shared__ float fac[ATT_MAX_SPLITS];
-  __shared__ float scratch[8];
-  const int unit = blockIdx.y, row = blockIdx.x;
-  const int group = a.hq / a.hkv;
-  const int h = CELLS ? unit % a.hkv : unit;
-  const int qt = CELLS ? unit / a.hkv : row / group, qh = h * group + (CELLS ? row : row % group);
-  const int64_t stride = (int64_t)a.units * a.rows * (D + 2);
-  const float* w0 = a.ws + ((int64_t)unit * a.rows + row) * (D + 2);
-  float m = -INFINITY;
-  for (int s = threadIdx.x; s < a.splits; s += blockDim.x) m = fmaxf(m, w0[s * stride]);
-  m = block_reduce(m, true, scratch);
-  const float base = m == -INFINITY ? 0.0f : m;
-  float l = 0.0f;
-  for (int s = threadIdx.x; s < a.splits; s += blockDim.x) {
-    const float f = exp2f(w0[s * stride] - base);
-    fac[s] = f;
-    l += w0[s * stride + 1] * f;
+  extern __shared__ float fac[];  // [splits][16]
+  __shared__ float s_inv[16];
+  constexpr int NDT = D / 16;
+  const int tid = threadIdx.x;
+  const int zgroups = CELLS ? 1 : (a.rows + 63) / 64;
+  const int dt = blockIdx.x, rt = blockIdx.y, unit = blockIdx.z / zgroups, zg = blockIdx.z % zgroups;
+  const int row0 = zg * 64 + rt * 16;
+  {
+    const int r = tid >> 4, j = tid & 15, row = row0 + r;
+    const bool real = row < a.rows;
+    const int64_t stride = (int64_t)a.units * a.rows;
+    const float* m0 = a.wm + (int64_t)unit * a.rows + row;
+    const float* l0 = a.wl + (int64_t)unit * a.rows + row;
+    float m = -INFINITY;
+    if (real)
+      for (int s2 = j; s2 < a.splits; s2 += 16) m = fmaxf(m, m0[s2 * stride]);
+#pragma unroll
+    for (int o = 1; o < 16; o <<= 1) m = fmaxf(m, __shfl_xor(m, o));
+    const float base = m == -INFINITY ? 0.0f : m;
+    float l = 0.0f;
+    for (int s2 = j; s2 < a.splits; s2 += 16) {
+      const float f = real ? exp2f(m0[s2 * stride] - base) : 0.0f;
+      fac[s2 * 16 + r] = f;
+      if (real) l += l0[s2 * stride] * f;
+    }
+#pragma unroll
+    for (int o = 1; o < 16; o <<= 1) l += __shfl_xor(l, o);
+    if (j == 0) s_inv[r] = l > 0.0f ? 1.0f / l : 0.0f;
   }
-  l = block_reduce(l, false, scratch);  // its barriers also publish fac
-  const float inv = l > 0.0f ? 1.0f / l : 0.0f;
-  XT* o = (XT*)a.out + ((int64_t)qt * a.hq + qh) * D;
-  for (int d = threadIdx.x; d < D; d += blockDim.x) {
-    float acc = 0.0f;
+  __syncthreads();
+  const int ln = tid >> 2, i = tid & 3, rr = 4 * (ln >> 4) + i, row = row0 + rr, dim = 16 * dt + (ln & 15);
+  const int64_t ostride = (int64_t)a.units * zgroups * 4 * NDT * 256;  // floats a split
+  const float* od = a.wo + ((((int64_t)unit * zgroups + zg) * 4 + rt) * NDT + dt) * 256 + tid;
+  float acc = 0.0f;
 #pragma unroll 8
-    for (int s = 0; s < a.splits; ++s) acc += w0[s * stride + 2 + d] * fac[s];
-    o[d] = from_f32<XT>(acc * inv);
+  for (int s2 = 0; s2 < a.splits; ++s2) acc += od[s2 * ostride] * fac[s2 * 16 + rr];
+  if (row < a.rows) {
+    const int group = a.hq / a.hkv;
+    const int h = CELLS ? unit % a.hkv : unit;
+    const int qt = CELLS ? unit / a.hkv : row / group, qh = h * group + (CELLS ? row : row % group);
+    ((XT*)a.out)[((int64_t)qt * a.hq + qh) * D + dim] = from_f32<XT>(acc * s_inv[rr]);
   }
 }
 
@@ -316,10 +316,10 @@ static int attn_cus() {
   return cus;
 }
 
-// splits of the context: enough blocks to fill the chip four times over, at least one step of tiles a split
-// (`min_tiles`), at most ATT_MAX_SPLITS splits
-static void plan_splits(AttnArgs& a, int zgroups, int min_tiles) {
-  const int64_t want = 4 * (int64_t)attn_cus();
+// splits of the context: one round of blocks over the chip (as many a CU as LDS holds), at least one step of
+// tiles a split (`min_tiles`), at most ATT_MAX_SPLITS splits
+static void plan_splits(AttnArgs& a, int zgroups, int min_tiles, int per_cu) {
+  const int64_t want = (int64_t)per_cu * attn_cus();
   const int64_t per_unit = std::max<int64_t>(1, want / ((int64_t)a.units * zgroups));
   int64_t tps = std::max<int64_t>(min_tiles, (a.tiles + per_unit - 1) / per_unit);
   tps = std::max<int64_t>(tps, (a.tiles + ATT_MAX_SPLITS - 1) / ATT_MAX_SPLITS);
@@ -336,13 +336,25 @@ template <int D, bool CELLS> static size_t attn_lds(int rows_here, int tiles_per
   const int PL = att_phases(rows_here);
   const size_t stage = 2 * (size_t)(2 * PL * att_part_bytes<D>());
   const size_t tabs = CELLS ? (size_t)tiles_per_split * 16 * 5 : (size_t)tiles_per_split * 4;
-  const size_t merge = sizeof(float) * (2 * ATT_WAVES * 64 + (size_t)ATT_WAVES * D * 16);
+  const size_t merge = PL > 1 ? sizeof(float) * (2 * ATT_WAVES * 64 + (size_t)ATT_WAVES * D * 16) : 0;
   return std::max(stage + ((tabs + 15) & ~(size_t)15), merge);
+}
+
+// tiles a split at least: a step of tiles, and enough that its partial outputs (rows x D floats) stay near a
+// quarter of its K and V (16 positions x D x 2 x 2 bytes a tile)
+static int att_min_tiles(int rows) { return std::max(att_phases(std::min(64, rows)), (std::min(64, rows) + 7) / 8); }
+
+// blocks a CU by LDS (the stage and the phase merge; the tables taken at 4 KiB)
+static int att_blocks_per_cu(int rows_here, int D) {
+  const int PL = att_phases(rows_here);
+  const size_t stage = 2 * (size_t)(2 * PL * 16 * D * 2) + 4096;
+  const size_t merge = PL > 1 ? sizeof(float) * (2 * ATT_WAVES * 64 + (size_t)ATT_WAVES * D * 16) : 0;
+  return (int)std::max<size_t>(1, std::min<size_t>(8, 160 * 1024 / std::max(stage, merge)));
 }
 
 template <typename XT, int D, bool CELLS> static int launch_attn(AttnArgs a, hipStream_t stream) {
   const int zgroups = CELLS ? 1 : (a.rows + 63) / 64;
-  plan_splits(a, zgroups, att_phases(std::min(64, a.rows)));
+  plan_splits(a, zgroups, att_min_tiles(a.rows), att_blocks_per_cu(std::min(64, a.rows), D));
   // the last row group may have fewer rows, more tile phases and so a larger stage
   const size_t lds = std::max(attn_lds<D, CELLS>(std::min(64, a.rows), a.tiles_per_split),
                               attn_lds<D, CELLS>(a.rows - 64 * (zgroups - 1), a.tiles_per_split));
@@ -351,16 +363,25 @@ template <typename XT, int D, bool CELLS> static int launch_attn(AttnArgs a, hip
   hipLaunchKernelGGL((k_attn_split<XT, D, CELLS>), dim3(a.splits, a.units, zgroups), dim3(ATT_NT), lds, stream, a);
   int st = check_launch("attention split");
   if (st) return st;
-  hipLaunchKernelGGL((k_attn_merge<XT, D, CELLS>), dim3(a.rows, a.units), dim3(std::min(D, 256)), 0, stream, a);
+  const int rtiles = (std::min(64, a.rows) + 15) / 16;  // row tiles of a row group (the last may hold fewer rows)
+  hipLaunchKernelGGL((k_attn_merge<XT, D, CELLS>), dim3(D / 16, rtiles, a.units * zgroups), dim3(256),
+                     (size_t)a.splits * 16 * sizeof(float), stream, a);
   return check_launch("attention merge");
 }
 
-static size_t attn_ws_bytes(int units, int rows, int tiles, int zgroups, int D) {
+// the workspace: max and sum a (split, unit, row), then the outputs (16-byte aligned) in the lanes' layout
+static size_t attn_ws_carve(AttnArgs* a_out, float* base, int units, int rows, int tiles, int zgroups, int D) {
   AttnArgs a{};
   a.units = units;
   a.tiles = tiles;
-  plan_splits(a, zgroups, att_phases(std::min(64, rows)));
-  return (size_t)a.splits * units * rows * (D + 2) * sizeof(float);
+  plan_splits(a, zgroups, att_min_tiles(rows), att_blocks_per_cu(std::min(64, rows), D));
+  const size_t ml = ((size_t)a.splits * units * rows + 3) & ~(size_t)3;  // floats, a multiple of 4
+  if (a_out) {
+    a_out->wm = base;
+    a_out->wl = base + ml;
+    a_out->wo = base + 2 * ml;
+  }
+  return (2 * ml + (size_t)a.splits * units * zgroups * 4 * D * 16) * sizeof(float);
 }
 
 }  // namespace sh
@@ -372,7 +393,8 @@ extern "C" {
 size_t sh_paged_attn_workspace(int64_t n_q, int64_t hq, int64_t hkv, int64_t head_dim, int64_t ctx_len) {
   if (n_q <= 0 || hkv <= 0 || hq % hkv || ctx_len <= 0) return 0;
   const int rows = (int)(n_q * (hq / hkv));
-  return attn_ws_bytes((int)hkv, rows, (int)((ctx_len + 15) / 16), (rows + 63) / 64, (int)head_dim);
+  return attn_ws_carve(nullptr, nullptr, (int)hkv, rows, (int)((ctx_len + 15) / 16), (rows + 63) / 64,
+                       (int)head_dim);
 }
 
 int sh_paged_attn(const void* q, const void* k_pages, const void* v_pages, const int32_t* page_table, int64_t n_pages,
@@ -412,6 +434,7 @@ int sh_paged_attn(const void* q, const void* k_pages, const void* v_pages, const
   a.units = (int)hkv;
   a.rows = (int)(n_q * (hq / hkv));
   a.scale_log2 = scale * 1.4426950408889634f;
+  attn_ws_carve(&a, (float*)workspace, a.units, a.rows, a.tiles, (a.rows + 63) / 64, (int)head_dim);
   return with_half_dtype(dtype, [&](auto* tp) {
     using XT = std::remove_pointer_t<decltype(tp)>;
     return head_dim == 256 ? launch_attn<XT, 256, false>(a, (hipStream_t)stream)
@@ -421,7 +444,8 @@ int sh_paged_attn(const void* q, const void* k_pages, const void* v_pages, const
 
 size_t sh_cells_attn_workspace(int64_t n_q, int64_t hq, int64_t hkv, int64_t head_dim, int64_t cells) {
   if (n_q <= 0 || hkv <= 0 || hq % hkv || cells <= 0) return 0;
-  return attn_ws_bytes((int)(n_q * hkv), (int)(hq / hkv), (int)((cells + 15) / 16), 1, (int)head_dim);
+  return attn_ws_carve(nullptr, nullptr, (int)(n_q * hkv), (int)(hq / hkv), (int)((cells + 15) / 16), 1,
+                       (int)head_dim);
 }
 
 int sh_cells_attn(const void* q, const void* k, const void* v, int64_t kv_len, const int32_t* cells,
@@ -461,6 +485,7 @@ int sh_cells_attn(const void* q, const void* k, const void* v, int64_t kv_len, c
   a.units = (int)(n_q * hkv);
   a.rows = (int)(hq / hkv);
   a.scale_log2 = scale * 1.4426950408889634f;
+  attn_ws_carve(&a, (float*)workspace, a.units, a.rows, a.tiles, 1, (int)head_dim);
   return with_half_dtype(dtype, [&](auto* tp) {
     using XT = std::remove_pointer_t<decltype(tp)>;
     return head_dim == 256 ? launch_attn<XT, 256, true>(a, (hipStream_t)stream)
