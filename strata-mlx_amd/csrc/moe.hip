@@ -459,7 +459,7 @@ template <int KIND> struct FrontItem {
 struct FrontPlan {
   int nbuf;      // ring slots
   int ring_off;  // after the IQ3_S table
-  int red_off;   // [2][7][64][TPG] floats: gate's and up's partial sums of waves 1..7
+  int red_off;   // [2][2][7][64][TPG] floats: gate's and up's partial sums of waves 1..7, the last two items
 };
 
 template <int KIND, typename XT, typename LT, int TPG>
@@ -630,21 +630,34 @@ __global__ __launch_bounds__(FRONT_WAVES * 64) void k_moe_front(
   const DecodeRegs kr = decode_regs<KIND, MT>();
   const int wcol = KIND == Q2_0 ? kq * GPER * 18 : (kq * GPER / 8) * 110;  // the wave's first group in a row
   constexpr int RED = 7 * 64 * TPG;  // up's partial sums after gate's
-  // an item's results are stored at the start of the next (after that item's wait: see the streaming matvec)
-  XT hv[TPG];
-  int hp[TPG], hrow = -1;
-  auto store_h = [&]() {
+  // An item's results are reduced and stored at the start of the next item, after its barrier, which also makes
+  // the other waves' partial sums (double-buffered) visible: one barrier an item. The stores go before the next
+  // loads are issued (a store counts on vmcnt like a load).
+  float pg[TPG], pu[TPG];
+  int hrow = -1, pbuf = 0;
+  auto finish = [&]() {
     if (wave == 0 && hrow >= 0) {
+      const int q = lane >> 4;
+      const float* rd = red + pbuf * 2 * RED + lane * TPG;
 #pragma unroll
-      for (int t = 0; t < TPG; ++t)
-        if (hp[t] >= 0) ((XT*)ws.h)[(int64_t)hp[t] * F + hrow] = hv[t];
+      for (int t = 0; t < TPG; ++t) {
+        float gs = pg[t], us = pu[t];
+#pragma unroll
+        for (int w = 0; w < FRONT_WAVES - 1; ++w) {
+          gs += rd[w * 64 * TPG + t];
+          us += rd[RED + w * 64 * TPG + t];
+        }
+        const int tt = q * TPG + t;
+        if (tt < n_tok)
+          ((XT*)ws.h)[(int64_t)s_wp[0][tt] * F + hrow] = swiglu_one(from_f32<XT>(gs), from_f32<XT>(us));
+      }
     }
   };
   for (int item = first; item < last; ++item) {
     const int ahead = min(fp.nbuf - 2, last - 1 - item);  // items issued after this one
     wait_vmcnt(ahead * loads);
     lds_sync();  // this item is in LDS for every wave; every wave is done with the item before
-    store_h();
+    finish();
     if (item + fp.nbuf - 1 < last) issue(item + fp.nbuf - 1);
     const int r = item - g0 * TILES;
     float acc_g[TPG], acc_u[TPG];
@@ -654,33 +667,25 @@ __global__ __launch_bounds__(FRONT_WAVES * 64) void k_moe_front(
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     item_mac<KIND, MT, TPG, GPER, true>(row0, IT::RSTRIDE, X, (const uint32_t*)lds, kr, acc_g);
     item_mac<KIND, MT, TPG, GPER, true>(row0 + 16 * IT::RSTRIDE, IT::RSTRIDE, X, (const uint32_t*)lds, kr, acc_u);
+    pbuf = item & 1;
     if (wave > 0) {
+      float* rw = red + pbuf * 2 * RED;
 #pragma unroll
       for (int t = 0; t < TPG; ++t) {
-        red[((wave - 1) * 64 + lane) * TPG + t] = acc_g[t];
-        red[RED + ((wave - 1) * 64 + lane) * TPG + t] = acc_u[t];
+        rw[((wave - 1) * 64 + lane) * TPG + t] = acc_g[t];
+        rw[RED + ((wave - 1) * 64 + lane) * TPG + t] = acc_u[t];
       }
-    }
-    lds_sync();
-    if (wave == 0) {
-      const int q = lane >> 4, n = lane & 15;
-      hrow = r * 16 + n;
+    } else {
 #pragma unroll
       for (int t = 0; t < TPG; ++t) {
-        const float* rd = red + lane * TPG + t;
-        float gs = acc_g[t], us = acc_u[t];
-#pragma unroll
-        for (int w = 0; w < FRONT_WAVES - 1; ++w) {
-          gs += rd[w * 64 * TPG];
-          us += rd[RED + w * 64 * TPG];
-        }
-        hv[t] = swiglu_one(from_f32<XT>(gs), from_f32<XT>(us));
-        const int tt = q * TPG + t;
-        hp[t] = tt < n_tok ? s_wp[0][tt] : -1;
+        pg[t] = acc_g[t];
+        pu[t] = acc_u[t];
       }
+      hrow = r * 16 + (lane & 15);
     }
   }
-  store_h();
+  lds_sync();
+  finish();
 }
 
 // the combine (strata_mlx/fused.py:448-462) of output (token t, row): experts in 8 rows j taking k = j, j + 8, ...,
@@ -733,7 +738,7 @@ template <int KIND> struct TailItem {
 struct TailPlan {
   int nbuf;      // ring slots
   int ring_off;  // after the IQ3_S table
-  int red_off;   // [4][64][TPG] floats: the second column half's sums
+  int red_off;   // [2][4][64][TPG] floats: the second column half's sums of the last two items
 };
 
 template <int KIND, typename XT, int TPG>
@@ -805,20 +810,26 @@ __global__ __launch_bounds__(FRONT_WAVES * 64) void k_moe_tail(const uint8_t* __
   x_finish<KIND, XT, TPG, GPER>(X, xraw);
 
   const DecodeRegs kr = decode_regs<KIND, MT>();
-  // each pair's outputs, rounded to the activation type, stored at the start of the next item; with the combine
-  // in this kernel as device-scope stores (written through the XCD's L2) for the block that combines them
-  XT yv[TPG];
-  int yp[TPG], yrow = -1;
+  // Each pair's outputs, rounded to the activation type, reduced and stored at the start of the next item, after
+  // its barrier, which also makes the other column half's sums (double-buffered) visible: one barrier an item.
+  // With the combine in this kernel they go out as device-scope stores (written through the XCD's L2) for the
+  // block that combines them.
+  float pacc[TPG];
+  int yrow = -1, pbuf = 0;
   auto store_y = [&]() {
-    if (yrow >= 0) {
+    if (kh == 0 && yrow >= 0) {
+      const int q = lane >> 4;
+      const float* rd = red + (pbuf * 4 * 64 + rg * 64 + lane) * TPG;
 #pragma unroll
       for (int t = 0; t < TPG; ++t) {
-        if (yp[t] < 0) continue;
-        float* at = ws.y + (int64_t)yp[t] * D + yrow;
+        const int tt = q * TPG + t;
+        if (tt >= n_tok) continue;
+        float* at = ws.y + (int64_t)s_wp[wave][tt] * D + yrow;
+        const float v = to_f32(from_f32<XT>(pacc[t] + rd[t]));
         if (combine)
-          __hip_atomic_store(at, to_f32(yv[t]), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          __hip_atomic_store(at, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         else
-          *at = to_f32(yv[t]);
+          *at = v;
       }
     }
   };
@@ -835,22 +846,17 @@ __global__ __launch_bounds__(FRONT_WAVES * 64) void k_moe_tail(const uint8_t* __
     const uint8_t* row0 = lds + tp.ring_off + (item % tp.nbuf) * IT::SLOT + rg * 16 * RB + wcol;
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     item_mac<KIND, MT, TPG, GPER, true>(row0, RB, X, (const uint32_t*)lds, kr, acc);
+    pbuf = item & 1;
     if (kh == 1) {
 #pragma unroll
-      for (int t = 0; t < TPG; ++t) red[(rg * 64 + lane) * TPG + t] = acc[t];
-    }
-    lds_sync();
-    if (kh == 0) {
-      const int q = lane >> 4, n = lane & 15;
-      yrow = tile * IT::ROWS + rg * 16 + n;
+      for (int t = 0; t < TPG; ++t) red[(pbuf * 4 * 64 + rg * 64 + lane) * TPG + t] = acc[t];
+    } else {
 #pragma unroll
-      for (int t = 0; t < TPG; ++t) {
-        const int tt = q * TPG + t;
-        yv[t] = from_f32<XT>(acc[t] + red[(rg * 64 + lane) * TPG + t]);
-        yp[t] = tt < n_tok ? s_wp[wave][tt] : -1;
-      }
+      for (int t = 0; t < TPG; ++t) pacc[t] = acc[t];
+      yrow = tile * IT::ROWS + rg * 16 + (lane & 15);
     }
   }
+  lds_sync();
   store_y();
   if (!combine) return;
   // Count this block's items into their row tiles' counters once every output of them is out (vmcnt 0: the
@@ -1064,7 +1070,7 @@ static int launch_moe(const uint8_t* gate, const uint8_t* up, const uint8_t* dow
     FrontPlan fp;
     const int nt = FRONT_WAVES * 64;
     fp.ring_off = moe_tab_bytes<KIND>();
-    const size_t red = (size_t)2 * 7 * 64 * TPG * 4;
+    const size_t red = (size_t)2 * 2 * 7 * 64 * TPG * 4;
     auto kern = k_moe_front<KIND, XT, LT, TPG>;
     const size_t fixed = static_lds(kern);
     // direct loads land below 128 KiB
@@ -1093,7 +1099,7 @@ static int launch_moe(const uint8_t* gate, const uint8_t* up, const uint8_t* dow
     tp.ring_off = moe_tab_bytes<KIND_DOWN>();
     auto kern = k_moe_tail<KIND_DOWN, XT, TPG>;
     const size_t fixed = static_lds(kern);
-    const size_t red = (size_t)4 * 64 * TPG * 4;
+    const size_t red = (size_t)2 * 4 * 64 * TPG * 4;
     tp.nbuf = 4;
     while (tp.nbuf > 2 && ((size_t)tp.ring_off + (size_t)tp.nbuf * IT::SLOT > 128 * 1024 ||
                            fixed + tp.ring_off + (size_t)tp.nbuf * IT::SLOT + red > LDS_BYTES))
