@@ -882,6 +882,72 @@ __global__ __launch_bounds__(FRONT_WAVES * 64) void k_moe_tail(const uint8_t* __
   if (tid < ncomb) __hip_atomic_store(&ws.cnt[s_comb[tid]], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// The tail for a window of few groups (at most 16: one token's k experts and the shared one), Q2_0: a block is 16
+// rows of down, a wave a group (all 512 columns; its 16 rows' bytes by direct loads into the wave's own LDS slot,
+// its tokens' activations in registers, all issued at once), each pair's 16 outputs rounded into LDS, then the
+// combine of those 16 rows for every token in LDS: no partial outputs through memory and no third launch.
+constexpr int TAIL1_WAVES = 16;
+
+template <typename XT, int TPG>
+__global__ __launch_bounds__(TAIL1_WAVES * 64) void k_moe_tail1(const uint8_t* __restrict__ down,
+                                                                 const uint8_t* __restrict__ sh_down, int K, int B,
+                                                                 MoeWs ws, XT* __restrict__ out) {
+  using MT = XT;
+  constexpr int E = FRONT_E, D = FRONT_D, F = FRONT_F;
+  constexpr int GPER = F / 64;                           // a wave's 16 rows whole: 8 Q2_0 blocks
+  constexpr int RB = (int)row_bytes_dev(Q2_0, F);       // 144 bytes: 16 rows at that stride in distinct banks
+  constexpr int CHUNKS = 16 * RB / 16, LOADS = (CHUNKS + 63) / 64, SLOT = LOADS * 1024;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int row0 = blockIdx.x * 16;
+  const int P = B * K;
+  __shared__ int s_groups, s_idx[16], s_gexp[TAIL1_WAVES], s_wp[TAIL1_WAVES][16];
+  __shared__ float s_w[16], s_gsh[MOE_MAX_TOKENS];
+  __shared__ float s_y[MOE_MAX_TOKENS * 2][16];  // [pair][row]: P + B <= 32 when the groups are at most 16
+  extern __shared__ u32x4 dyn[];
+  uint8_t* lds = (uint8_t*)dyn;
+  const uint32_t lds_base = SH_LDS_ADDR(dyn);
+
+  if (tid == 0) s_groups = *ws.n_groups;
+  if (tid < P) {
+    s_idx[tid] = ws.idx[tid];
+    s_w[tid] = ws.w[tid];
+  }
+  if (tid < TAIL1_WAVES) s_gexp[tid] = ws.g_expert[min(tid, P)];  // entries past the groups are never read
+  if (tid < B) s_gsh[tid] = ws.gsh[tid];
+  __syncthreads();
+  const int groups = s_groups;
+  if (wave < groups) {
+    const int e = __builtin_amdgcn_readfirstlane(s_gexp[wave]);
+    const uint8_t* src = (e == E ? sh_down : down + (int64_t)e * D * RB) + (int64_t)row0 * RB;
+    const uint32_t buf = lds_base + wave * SLOT;
+#pragma unroll
+    for (int j = 0; j < LOADS; ++j) lds_dma16(src, 16 * min(j * 64 + lane, CHUNKS - 1), buf + j * 1024);
+    const int n_tok = group_pairs(e, E, s_idx, B, K, s_wp[wave]);
+    int mt = lane_token<TPG>();
+    mt = mt < n_tok ? mt : 0;
+    XRegs<Q2_0, TPG, GPER> X;
+    load_x_row<Q2_0, XT, TPG, GPER, true>(X, (const XT*)ws.h + (int64_t)s_wp[wave][mt] * F, 0);
+    const DecodeRegs kr = decode_regs<Q2_0, MT>();
+    wait_vmcnt(0);
+    float acc[TPG];
+#pragma unroll
+    for (int t = 0; t < TPG; ++t) acc[t] = 0.0f;
+    item_mac<Q2_0, MT, TPG, GPER, true>(lds + wave * SLOT, RB, X, nullptr, kr, acc);
+    const int q = lane >> 4, n = lane & 15;
+#pragma unroll
+    for (int t = 0; t < TPG; ++t) {
+      const int tt = q * TPG + t;
+      if (tt < n_tok) s_y[s_wp[wave][tt]][n] = to_f32(from_f32<XT>(acc[t]));
+    }
+  }
+  __syncthreads();
+  if (tid < B * 16) {
+    const int t = tid >> 4, n = tid & 15;
+    combine_one<XT>(t, row0 + n, K, B, ws, out, [&](int p) { return s_y[p][n]; });
+  }
+}
+
 // the combine as a kernel of its own after the tail, a thread an output
 template <typename XT>
 __global__ __launch_bounds__(256) void k_moe_combine(int K, int B, MoeWs ws, XT* __restrict__ out) {
@@ -1118,6 +1184,15 @@ static int launch_moe(const uint8_t* gate, const uint8_t* up, const uint8_t* dow
     // a few tokens: the tail's last block of a row tile combines it (no third launch); more: a combine kernel
     // (the tiles' last blocks would each combine several tiles, serially)
     const int combine = B <= TAIL_COMBINE_UPTO;
+    if constexpr (KIND_DOWN == Q2_0) {
+      if (std::min<int64_t>(B * K, E) + 1 <= TAIL1_WAVES) {  // few groups: a block a 16-row tile, a wave a group
+        constexpr int LOADS = (16 * (int)row_bytes_dev(Q2_0, FRONT_F) / 16 + 63) / 64;
+        const size_t lds1 = (size_t)TAIL1_WAVES * LOADS * 1024;
+        hipLaunchKernelGGL((k_moe_tail1<XT, TPG>), dim3(FRONT_D / 16), dim3(TAIL1_WAVES * 64), lds1, stream, down, sd,
+                           (int)K, (int)B, ws, out);
+        return check_launch("moe_decode tail");
+      }
+    }
     hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(nt), lds, stream, down, sd, (int)K, (int)B, tp, stab, ws,
                        combine, out);
     st = check_launch("moe_decode tail");

@@ -182,3 +182,27 @@ def test_the_benchmark_shape_chooses_among_ties_by_index(logit_dtype, c3_layers,
     np.testing.assert_array_equal(idx.cpu().numpy(), want_idx)
     np.testing.assert_allclose(wt.cpu().numpy(), want_w, rtol=2e-6, atol=1e-7)
     assert rel_err(out.float().cpu(), want) <= 1e-2
+
+
+@pytest.mark.parametrize("tokens, k, dtype", [(1, 10, torch.bfloat16), (2, 7, torch.bfloat16), (3, 5, torch.float16),
+                                              (1, 15, torch.float16)])
+def test_the_benchmark_shape_with_few_groups(tokens, k, dtype, c3_layers, tables, dev):
+    """At most 16 groups (the shared expert and the tokens' experts): the tail takes a wave a group and combines
+    in LDS; against the oracle as every other window."""
+    E, D, F = 512, 2048, 512
+    fetch, lin, shared = c3_layers[("Q2_0", "Q2_0")]
+    rng = np.random.default_rng(tokens * 31 + k)
+    name = "bfloat16" if dtype == torch.bfloat16 else "float16"
+    x = torch.from_numpy(rng.standard_normal((tokens, D)).astype(np.float32)).to(dtype)
+    logits = torch.from_numpy(rng.standard_normal((tokens, E)).astype(np.float32)).to(dtype)
+    wg = torch.from_numpy(rng.standard_normal(D).astype(np.float32) * 0.05).to(dtype)
+    moe = SF.MoEDecode(lin["gate"], lin["up"], lin["down"], lin["sgate"], lin["sup"], lin["sdown"], wg.to(dev), k)
+    out, idx, wt = moe(logits.to(dev), x.to(dev), want_choice=True)
+    want, want_idx, want_w = OM.moe_decode_blocks(logits.float().numpy(), x.float().numpy(), k, fetch,
+                                                  ("Q2_0", "Q2_0"), (E, D, F), shared, wg.float().numpy(), tables,
+                                                  name)
+    np.testing.assert_array_equal(idx.cpu().numpy(), want_idx)
+    np.testing.assert_allclose(wt.cpu().numpy(), want_w, rtol=2e-6, atol=1e-7)
+    assert rel_err(out.float().cpu(), want) <= 1e-2
+    for _ in range(2):
+        assert torch.equal(moe(logits.to(dev), x.to(dev)), out)
