@@ -689,16 +689,17 @@ __global__ __launch_bounds__(FRONT_WAVES * 64) void k_moe_front(
 }
 
 // the combine (strata_mlx/fused.py:448-462) of output (token t, row): experts in 8 rows j taking k = j, j + 8, ...,
-// each product rounded as the reference rounds it, then the shared expert gated. y(p) reads pair p's output.
-template <typename XT, typename YF>
-__device__ __forceinline__ void combine_one(int t, int row, int K, int B, const MoeWs& ws, XT* out, YF&& y) {
+// each product rounded as the reference rounds it, then the shared expert gated (its gate logit gsh). y(p) and w(p)
+// read pair p's output and routing weight.
+template <typename XT, typename YF, typename WF>
+__device__ __forceinline__ void combine_one(int t, int row, int K, int B, float gsh, XT* out, YF&& y, WF&& w) {
 #pragma clang fp contract(off)
   constexpr int D = FRONT_D;
   float yk[16], wk[16];  // k <= 16
 #pragma unroll
   for (int kk = 0; kk < 16; ++kk) {
     yk[kk] = kk < K ? y(t * K + kk) : 0.0f;
-    wk[kk] = kk < K ? ws.w[t * K + kk] : 0.0f;
+    wk[kk] = kk < K ? w(t * K + kk) : 0.0f;
   }
   const float ys = y(B * K + t);
   float acc = 0.0f;
@@ -718,7 +719,7 @@ __device__ __forceinline__ void combine_one(int t, int row, int K, int B, const 
     }
   }
   const XT routed = from_f32<XT>(acc);
-  const XT gate = from_f32<XT>(1.0f / (1.0f + expf(-ws.gsh[t])));
+  const XT gate = from_f32<XT>(1.0f / (1.0f + expf(-gsh)));
   const XT shared = from_f32<XT>(to_f32(gate) * ys);
   out[(int64_t)t * D + row] = from_f32<XT>(to_f32(routed) + to_f32(shared));
 }
@@ -875,9 +876,9 @@ __global__ __launch_bounds__(FRONT_WAVES * 64) void k_moe_tail(const uint8_t* __
   for (int qv = tid; qv < ncomb * B * IT::ROWS; qv += NT) {
     const int c = qv / (B * IT::ROWS), rest = qv - c * (B * IT::ROWS);
     const int t = rest / IT::ROWS, row = s_comb[c] * IT::ROWS + rest % IT::ROWS;
-    combine_one<XT>(t, row, K, B, ws, out, [&](int p) {
+    combine_one<XT>(t, row, K, B, ws.gsh[t], out, [&](int p) {
       return __hip_atomic_load(ws.y + (int64_t)p * D + row, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    });
+    }, [&](int p) { return ws.w[p]; });
   }
   if (tid < ncomb) __hip_atomic_store(&ws.cnt[s_comb[tid]], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
@@ -944,7 +945,8 @@ __global__ __launch_bounds__(TAIL1_WAVES * 64) void k_moe_tail1(const uint8_t* _
   __syncthreads();
   if (tid < B * 16) {
     const int t = tid >> 4, n = tid & 15;
-    combine_one<XT>(t, row0 + n, K, B, ws, out, [&](int p) { return s_y[p][n]; });
+    combine_one<XT>(t, row0 + n, K, B, s_gsh[t], out, [&](int p) { return s_y[p][n]; },
+                    [&](int p) { return s_w[p]; });
   }
 }
 
@@ -952,7 +954,8 @@ __global__ __launch_bounds__(TAIL1_WAVES * 64) void k_moe_tail1(const uint8_t* _
 template <typename XT>
 __global__ __launch_bounds__(256) void k_moe_combine(int K, int B, MoeWs ws, XT* __restrict__ out) {
   const int row = blockIdx.x * 256 + threadIdx.x;
-  combine_one<XT>(blockIdx.y, row, K, B, ws, out, [&](int p) { return ws.y[(int64_t)p * FRONT_D + row]; });
+  combine_one<XT>(blockIdx.y, row, K, B, ws.gsh[blockIdx.y], out, [&](int p) { return ws.y[(int64_t)p * FRONT_D + row]; },
+                  [&](int p) { return ws.w[p]; });
 }
 
 // ---- down and the combine: a block is 16 output rows of every group's expert
