@@ -161,6 +161,22 @@ int sh_moe_decode_phase(int phase, int kind, int kind_down, const void* gate, co
 int sh_tile_matmul(int kind, const void* blocks, const void* tables, int64_t experts, int64_t rows, int64_t cols,
                    const void* a, int a_dtype, int64_t pairs, const int32_t* tile_expert, float* out, void* stream);
 
+/* strata_mlx/blocks.py:566-574 (_tiled_glu: a = x[token]; h = swiglu(tile_matmul(gate, a), tile_matmul(up, a))
+ * .astype(x.dtype)) in one pass: h[s] = x_dtype(silu(g) * u), g / u = gate / up of tile_expert[s / 16] . x[token[s]]
+ * with the weights rounded to x's type and float32 sums. gate and up: stacks of `experts` (rows, cols) layers of
+ * Q2_0 or IQ3_S; x (tokens, cols) bfloat16 / float16; token, h: `slots` (a multiple of 16) entries / rows; rows
+ * % 32 == 0, cols % 256 == 0. Tokens outside 0..tokens-1 are clamped; tiles naming no expert leave their rows. */
+int sh_tile_glu(int kind, const void* gate, const void* up, const void* tables, int64_t experts, int64_t rows,
+                int64_t cols, const void* x, int x_dtype, int64_t tokens, const int32_t* token, int64_t slots,
+                const int32_t* tile_expert, void* h, void* stream);
+
+/* strata_mlx/blocks.py:575 (out = tile_matmul(down, h)[where].astype(x.dtype)) in one pass: for each slot s with
+ * pair[s] in 0..pairs-1, out[pair[s]] = h_dtype(down of tile_expert[s / 16] . h[s]) (pair = the inverse of
+ * tiles_of's `where`, -1 for slots no pair fills). down: Q2_0 or IQ3_S, rows % 64 == 0, cols % 256 == 0. */
+int sh_tile_down(int kind, const void* down, const void* tables, int64_t experts, int64_t rows, int64_t cols,
+                 const void* h, int h_dtype, int64_t slots, const int32_t* tile_expert, const int32_t* pair,
+                 int64_t pairs, void* out, void* stream);
+
 /* ---- decode attention (strata_mlx/attention.py:118-165) */
 
 /* _gathered over a page table (attention.py:144-165 with cells = page_table[p / 16] * 16 + p % 16): q (n_q, hq,

@@ -189,6 +189,384 @@ static int launch_tiles(const uint8_t* blocks, const uint8_t* tables, int64_t ex
   return check_launch("tile_matmul");
 }
 
+
+// ---- the streaming form (Q2_0 and IQ3_S, columns in chunks of 256, rows in blocks of 64)
+//
+// Persistent blocks, one a CU. A block first lays its window of tiles out in units: a unit is at most TS_TGU
+// consecutive tiles of one expert, a run of one expert's tiles cut every TS_TGU tiles from its start; tiles that
+// name no expert make no unit. Every block computes the same list, then takes the items (unit, block of 64 rows)
+// blockIdx.x, blockIdx.x + gridDim.x, ... All its items' chunks form one stream. Waves 0-7 (producers) bring chunk
+// after chunk of 256 columns of the item's 64 rows of blocks into an LDS ring by direct loads, TS_LEAD chunks
+// ahead, and dequantize each into one of two bf16 / fp16 buffers; waves 8-15 (consumers) multiply the other
+// buffer on MFMA, all 64 rows against one tile each, their activation fragments loaded two steps ahead. Only consumers issue ordinary loads, so the
+// compiler's waits for them never wait on the ring's loads. A step is one barrier: producers have landed chunk
+// q + 1 and dequantize it while consumers multiply chunk q.
+//
+// Modes: TS_PLAIN is tile_matmul (a in slot order, float32 rows of the slots out); TS_GLU takes a token's row of
+// x for each slot, runs gate and up (32 rows of each an item) and writes silu(g) * u rounded to x's type in slot
+// order; TS_DOWN takes those rows and writes each pair's row, rounded to x's type, where the slot's pair is.
+enum { TS_PLAIN = 0, TS_GLU = 1, TS_DOWN = 2 };
+constexpr int TS_KCH = 256, TS_RBV = 64, TS_TGU = 8, TS_NR = 6, TS_LEAD = 5, TS_NT = 1024;
+constexpr int TS_WT = 3 * TS_NT;                      // tiles of a window: three a thread in the layout
+constexpr int TS_PPR = 8;                             // 16-byte pieces a row's chunk may cover
+constexpr int TS_SLOT = TS_RBV * TS_PPR * 16;         // bytes of a ring slot: one piece a producer lane
+constexpr int TS_BUF = TS_RBV * TS_KCH;               // elements of a dequantized chunk
+static_assert(TS_NR >= TS_LEAD + 1, "a ring slot is reloaded only after a barrier past its dequantization");
+static_assert(TS_WT <= 4096 && TS_TGU < 16, "a unit packs its first tile in 12 bits and its length in 4");
+static_assert(TS_SLOT == 512 * 16 && TS_RBV * (TS_KCH / 32) == 512, "a piece and a run of 32 a producer lane");
+
+struct TileStreamArgs {
+  const uint8_t* w0;           // the stack (gate for TS_GLU)
+  const uint8_t* w1;           // up (TS_GLU)
+  const uint8_t* tables;       // the codebook blob (IQ3_S: its signed table)
+  const void* a;               // TS_PLAIN / TS_DOWN: (slots, cols); TS_GLU: x (tokens, cols)
+  const int32_t* token;        // TS_GLU: the row of x of each slot
+  const int32_t* pair;         // TS_DOWN: the output row of each slot, or -1
+  const int32_t* tile_expert;  // (n_tiles,)
+  void* out;
+  int64_t n_src;               // TS_GLU: rows of x (tokens are clamped into them); TS_DOWN: output rows (pairs)
+  int experts, rows, cols, rbytes, n_tiles;
+  int tile0;                   // the first tile of this launch's window of at most TS_WT tiles
+};
+
+template <int KIND> __host__ __device__ constexpr int ts_chunk_bytes() { return TS_KCH / wpb(KIND) * bpb(KIND); }
+template <int KIND> __host__ __device__ constexpr int ts_tab_bytes() { return KIND == IQ3_S ? IQ3S_SIGNED_BYTES : 0; }
+// LDS: [table][ring][two dequantized chunks][tile experts of the window][units of the window][scan scratch]
+template <int KIND, typename XT> __host__ __device__ constexpr int ts_lds_bytes() {
+  return ts_tab_bytes<KIND>() + TS_NR * TS_SLOT + 2 * TS_BUF * (int)sizeof(XT) + TS_WT * 2 + TS_WT * 2 + 64;
+}
+
+// a position in a block's stream: chunk c of item (unit u, row block rb), and the unit's first tile, length and
+// expert; advanced chunk by chunk without divisions
+struct TsCursor {
+  int q, c, u, rb, start, len, e;
+};
+
+// exclusive scan over the block (MAX: running maximum, identity -1; else running sum), and the total
+// x, which the compiler cannot see through: values computed from it in a loop stay in the loop
+__device__ __forceinline__ int opaque(int x) {
+  asm volatile("" : "+v"(x));
+  return x;
+}
+
+template <bool MAX> __device__ __forceinline__ int ts_block_scan(int v, int* scr, int& total) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  int inc = v;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const int o = __shfl_up(inc, d);
+    if (lane >= d) inc = MAX ? max(inc, o) : inc + o;
+  }
+  if (lane == 63) scr[wave] = inc;
+  __syncthreads();
+  int pre = MAX ? -1 : 0, tot = MAX ? -1 : 0;
+#pragma unroll
+  for (int w = 0; w < TS_NT / 64; ++w) {
+    const int s = scr[w];
+    if (w < wave) pre = MAX ? max(pre, s) : pre + s;
+    tot = MAX ? max(tot, s) : tot + s;
+  }
+  __syncthreads();
+  int ex = __shfl_up(inc, 1);
+  if (lane == 0) ex = MAX ? -1 : 0;
+  total = tot;
+  return MAX ? max(pre, ex) : pre + ex;
+}
+
+template <int KIND, typename XT, int MODE>
+__global__ __launch_bounds__(TS_NT) void k_tile_stream(TileStreamArgs g) {
+  constexpr int CB = ts_chunk_bytes<KIND>(), TAB = ts_tab_bytes<KIND>(), TPT = TS_WT / TS_NT;
+  constexpr int VR = MODE == TS_GLU ? TS_RBV / 2 : TS_RBV;  // rows of one stack an item
+  static_assert(CB + 15 <= TS_PPR * 16, "a row's chunk fits its ring row");
+  extern __shared__ u32x4 dyn[];
+  uint8_t* lds = (uint8_t*)dyn;
+  uint8_t* tab = lds;
+  uint8_t* ring = lds + TAB;
+  XT* wl = (XT*)(ring + TS_NR * TS_SLOT);
+  int16_t* s_te = (int16_t*)(wl + 2 * TS_BUF);  // expert of each tile of the window, -1 for none
+  uint16_t* s_unit = (uint16_t*)(s_te + TS_WT);
+  int* s_scr = (int*)(s_unit + TS_WT);
+  const uint32_t ring_lds = SH_LDS_ADDR(dyn) + TAB;
+
+  const int tid = threadIdx.x, lane = tid & 63, n = lane & 15, gq = lane >> 4;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int nch = g.cols / TS_KCH, rblk = g.rows / VR;
+  const int64_t rbytes = g.rbytes;
+
+  if constexpr (KIND == IQ3_S) {  // the signed table, once a block
+    const uint8_t* src = g.tables + TAB_IQ3S_SIGNED;
+    constexpr int PIECES = IQ3S_SIGNED_BYTES / 16;
+#pragma unroll
+    for (int i = 0; i < (PIECES + TS_NT - 1) / TS_NT; ++i)
+      if (i * TS_NT + wave * 64 < PIECES)  // whole waves: PIECES is a multiple of 64
+        lds_dma16(src, (uint32_t)((i * TS_NT + tid) * 16), SH_LDS_ADDR(dyn) + (uint32_t)((i * TS_NT + wave * 64) * 16));
+  }
+
+  {
+    // ---- the window's units (one window a launch: a loop around both roles would let the compiler's waits
+    // for one role's loads reach into the other's code)
+    const int w0 = g.tile0, nwin = min(TS_WT, g.n_tiles - w0);
+    for (int i = tid; i < TS_WT; i += TS_NT) {
+      const int e = i < nwin ? g.tile_expert[w0 + i] : -1;
+      s_te[i] = (int16_t)((e >= 0 && e < g.experts) ? e : -1);
+    }
+    __syncthreads();
+    int ex[TPT], rsl[TPT];
+    int carry = -1;
+#pragma unroll
+    for (int j = 0; j < TPT; ++j) {
+      const int i = TPT * tid + j;
+      ex[j] = s_te[i];
+      if (i == 0 || ex[j] != s_te[i - 1]) carry = i;  // a run of one expert (or of none) starts here
+      rsl[j] = carry;
+    }
+    int ignore;
+    const int carry_in = ts_block_scan<true>(carry, s_scr, ignore);
+    int cnt = 0;
+    bool seg[TPT], unit[TPT];
+#pragma unroll
+    for (int j = 0; j < TPT; ++j) {
+      const int i = TPT * tid + j, r = rsl[j] >= 0 ? rsl[j] : carry_in;
+      seg[j] = (i - r) % TS_TGU == 0;
+      unit[j] = seg[j] && ex[j] >= 0 && i < nwin;
+      cnt += unit[j];
+    }
+    uint8_t* s_seg = (uint8_t*)wl;  // segment starts, in the first dequantization buffer until the stream
+#pragma unroll
+    for (int j = 0; j < TPT; ++j) s_seg[TPT * tid + j] = seg[j];
+    int n_units;
+    int pos = ts_block_scan<false>(cnt, s_scr, n_units);  // (its barriers publish s_seg)
+#pragma unroll
+    for (int j = 0; j < TPT; ++j) {
+      const int i = TPT * tid + j;
+      if (unit[j]) {
+        int len = 1;
+        while (len < TS_TGU && i + len < nwin && !s_seg[i + len]) ++len;
+        s_unit[pos++] = (uint16_t)(i | (len << 12));
+      }
+    }
+    __syncthreads();
+
+    // ---- the stream of this block's items' chunks
+    const int n_items = n_units * rblk;
+    const int my_items = n_items > (int)blockIdx.x ? (n_items - 1 - (int)blockIdx.x) / (int)gridDim.x + 1 : 0;
+    const int Q = my_items * nch;
+    if (Q == 0) {
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // no load into LDS outlives the block
+      return;
+    }
+    const int G = (int)gridDim.x, gdiv = G / rblk, gmod = G - gdiv * rblk;
+    auto cur_fill = [&](TsCursor& k) {
+      const int uu = s_unit[k.u];
+      k.start = w0 + (uu & 4095);
+      k.len = uu >> 12;
+      k.e = s_te[uu & 4095];
+    };
+    auto cur_at = [&](int q) {
+      TsCursor k;
+      k.q = q;
+      const int kk = q / nch, item = (int)blockIdx.x + kk * G;
+      k.c = q - kk * nch;
+      k.u = item / rblk;
+      k.rb = item - k.u * rblk;
+      k.start = k.len = k.e = 0;
+      if (q < Q) cur_fill(k);
+      return k;
+    };
+    auto cur_next = [&](TsCursor& k) {
+      ++k.q;
+      if (++k.c == nch) {
+        k.c = 0;
+        k.rb += gmod;
+        k.u += gdiv;
+        if (k.rb >= rblk) k.rb -= rblk, ++k.u;
+        if (k.q < Q) cur_fill(k);
+      }
+    };
+
+    if (wave < 8) {
+      // ---- producers: the ring and the dequantization; lane (row v, piece / run j). The lane's offsets are
+      // recomputed each step from an opaque copy of the thread index: hoisted out of the loop they would stay
+      // live through the consumers' loop as well and spill.
+      auto row_src = [&](const TsCursor& s, int v) {  // the first byte of row v's chunk
+        const uint8_t* stack = g.w0;
+        int r = s.rb * VR + v;
+        if constexpr (MODE == TS_GLU) {
+          stack = v < VR ? g.w0 : g.w1;
+          r = s.rb * VR + (v & (VR - 1));
+        }
+        return stack + ((int64_t)s.e * g.rows + r) * rbytes + (int64_t)s.c * CB;
+      };
+      auto issue = [&](const TsCursor& k) {  // chunk k.q into ring slot k.q % TS_NR: piece j of row v
+        const int t = opaque(tid), v = t >> 3, j = t & 7, q = k.q;
+        const uint8_t* src = row_src(k, v);
+        const int lead = (int)((uintptr_t)src & 15);
+        if (16 * j < lead + CB)
+          lds_dma16p(src - lead + 16 * j, ring_lds + (uint32_t)((q % TS_NR) * TS_SLOT + wave * 1024));
+      };
+      auto dequant = [&](const TsCursor& k) {  // chunk k.q into buffer k.q & 1: run j of row v
+        const int t = opaque(tid), v = t >> 3, j = t & 7, q = k.q;
+        const uint8_t* src = row_src(k, v);
+        const uint8_t* raw = ring + (q % TS_NR) * TS_SLOT + v * (TS_PPR * 16) + ((uintptr_t)src & 15);
+        u32x4 w[4];
+        dequant_run<KIND, XT>(raw, j, tab, w);
+        XT* dst = wl + (q & 1) * TS_BUF + v * TS_KCH;
+#pragma unroll
+        for (int h = 0; h < 4; ++h) *(u32x4*)(dst + 8 * ((4 * j + h) ^ (v & 15))) = w[h];
+      };
+      const int lead0 = min(TS_LEAD, Q);
+      TsCursor ci = cur_at(0), cd = cur_at(0);  // the next chunk to load, the next to dequantize
+      for (int q = 0; q < lead0; ++q) {
+        issue(ci);
+        cur_next(ci);
+      }
+      if constexpr (KIND == IQ3_S) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // (the table, and the lead)
+      wait_vmcnt(lead0 - 1);
+      lds_sync();
+      dequant(cd);
+      cur_next(cd);
+      for (int q = 0; q < Q; ++q) {
+        if (ci.q < Q) {  // ci.q == q + TS_LEAD
+          issue(ci);
+          cur_next(ci);
+        }
+        if (q + 1 < Q) wait_vmcnt(max(0, min(q + TS_LEAD, Q - 1) - (q + 1)));
+        lds_sync();
+        if (cd.q < Q) {  // cd.q == q + 1
+          dequant(cd);
+          cur_next(cd);
+        }
+      }
+    } else {
+      // ---- consumers: the 64 rows (four fragments of 16) against tile cw of the unit; the fragments of
+      // chunk q in af[q & 1], loaded two steps ahead (the loop is unrolled by two: the buffers stay registers)
+      const int cw = wave - 8;
+      const XT* a = (const XT*)g.a;
+      f32x4 acc[4];
+      u32x4 af[2][TS_KCH / 32];
+      const XT* arow = a;
+#pragma unroll
+      for (int f = 0; f < 4; ++f) acc[f] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+      auto load_a = [&](const TsCursor& s, auto bc) {  // chunk s.q's fragments of the lane's row into af[bc]
+        constexpr int BUF = decltype(bc)::value;
+        const int ln = opaque(lane), n = ln & 15, gq = ln >> 4;
+        if (cw < s.len) {
+          if (s.c == 0) {  // a new item: the row of the lane's slot
+            const int64_t slot = (int64_t)(s.start + cw) * TILE_TOKENS + n;
+            int64_t row = slot;
+            if constexpr (MODE == TS_GLU) row = min(max((int64_t)g.token[slot], (int64_t)0), g.n_src - 1);
+            arow = a + row * g.cols;
+          }
+#pragma unroll
+          for (int ks = 0; ks < TS_KCH / 32; ++ks)
+            af[BUF][ks] = *(const u32x4*)(arow + s.c * TS_KCH + ks * 32 + 8 * gq);
+        } else {  // (defined on every path: the fragments are not live across the epilogue)
+#pragma unroll
+          for (int ks = 0; ks < TS_KCH / 32; ++ks) af[BUF][ks] = u32x4{0u, 0u, 0u, 0u};
+        }
+      };
+      TsCursor cs = cur_at(0), cl = cur_at(0);  // the chunk to multiply, the next to load fragments of
+      auto step = [&](auto bc) {
+        constexpr int BUF = decltype(bc)::value;
+        const TsCursor& s = cs;
+        const int q = s.q;
+        lds_sync();
+        const XT* wb = wl + (q & 1) * TS_BUF;
+        if (cw < s.len) {
+          const int ln = opaque(lane), n = ln & 15;
+#pragma unroll
+          for (int ks = 0; ks < TS_KCH / 32; ++ks) {
+            const int gq = ln >> 4;
+            u32x4 b[4];
+#pragma unroll
+            for (int f = 0; f < 4; ++f) {
+              const int r = 16 * f + n;
+              b[f] = *(const u32x4*)(wb + r * TS_KCH + 8 * ((4 * ks + gq) ^ (r & 15)));
+            }
+#pragma unroll
+            for (int f = 0; f < 4; ++f) acc[f] = mfma<XT>(af[BUF][ks], b[f], acc[f]);
+          }
+          if (s.c == nch - 1) {  // the item's rows are done
+            const int gq = ln >> 4;
+            const int64_t slot0 = (int64_t)(s.start + cw) * TILE_TOKENS + 4 * gq;
+            int pr[4] = {0, 0, 0, 0};  // TS_DOWN: the slots' output rows, loaded before any store
+            if constexpr (MODE == TS_DOWN) {
+#pragma unroll
+              for (int i = 0; i < 4; ++i) pr[i] = g.pair[slot0 + i];
+            }
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              if constexpr (MODE == TS_PLAIN) {
+                float* o = (float*)g.out + (slot0 + i) * g.rows + s.rb * VR + n;
+#pragma unroll
+                for (int f = 0; f < 4; ++f) o[16 * f] = acc[f][i];
+              } else if constexpr (MODE == TS_GLU) {
+                XT* o = (XT*)g.out + (slot0 + i) * g.rows + s.rb * VR + n;
+#pragma unroll
+                for (int f = 0; f < 2; ++f) {
+                  const float gt = acc[f][i], up = acc[f + 2][i];
+                  o[16 * f] = from_f32<XT>(gt / (1.0f + expf(-gt)) * up);
+                }
+              } else {
+                const int p = pr[i];
+                if (p >= 0 && p < g.n_src) {
+                  XT* o = (XT*)g.out + (int64_t)p * g.rows + s.rb * VR + n;
+#pragma unroll
+                  for (int f = 0; f < 4; ++f) o[16 * f] = from_f32<XT>(acc[f][i]);
+                }
+              }
+            }
+#pragma unroll
+            for (int f = 0; f < 4; ++f) acc[f] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+          }
+        }
+        __builtin_amdgcn_sched_barrier(0);  // chunk q + 2's fragments load after chunk q's are consumed
+        cur_next(cs);
+        if (cl.q < Q) {  // cl.q == q + 2
+          load_a(cl, bc);
+          cur_next(cl);
+        }
+      };
+      using B0 = std::integral_constant<int, 0>;
+      using B1 = std::integral_constant<int, 1>;
+      load_a(cl, B0{});
+      cur_next(cl);
+      if (Q > 1) {
+        load_a(cl, B1{});
+        cur_next(cl);
+      }
+      if constexpr (KIND == IQ3_S) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // (the table)
+      lds_sync();
+      int q = 0;
+      for (; q + 1 < Q; q += 2) {
+        step(B0{});
+        step(B1{});
+      }
+      if (q < Q) step(B0{});
+      // nothing of the consumers' left in flight where the compiler joins the roles' paths: its waits in the
+      // producers' code would count against their ring loads
+      __builtin_amdgcn_s_waitcnt(0);
+    }
+  }
+}
+
+template <int KIND, typename XT, int MODE>
+static int launch_stream(const TileStreamArgs& g, hipStream_t stream, const char* what) {
+  constexpr size_t lds = ts_lds_bytes<KIND, XT>();
+  static_assert(lds <= 160 * 1024, "the stream's LDS fits a CU");
+  auto kern = k_tile_stream<KIND, XT, MODE>;
+  if (lds + static_lds(kern) > LDS_BYTES) return fail(E_UNSUPPORTED, "%s: %zu bytes of LDS", what, lds);
+  if (g.experts > 32767) return fail(E_UNSUPPORTED, "%s: %d experts (at most 32767)", what, g.experts);
+  for (int w0 = 0; w0 < g.n_tiles; w0 += TS_WT) {
+    TileStreamArgs gw = g;
+    gw.tile0 = w0;
+    hipLaunchKernelGGL(kern, dim3((unsigned)device_cus()), dim3(TS_NT), lds, stream, gw);
+    const int st = check_launch(what);
+    if (st) return st;
+  }
+  return OK;
+}
+
 }  // namespace sh
 
 using namespace sh;
@@ -212,6 +590,21 @@ int sh_tile_matmul(int kind, const void* blocks, const void* tables, int64_t exp
   if (((uintptr_t)a & 15) || ((uintptr_t)blocks & 15))
     return fail(E_ARG, "tile_matmul: activations and blocks must be 16-byte aligned");
   const int64_t n_tiles = pairs / TILE_TOKENS;
+  if (kind == IQ3_S || kind == Q2_0) {
+    TileStreamArgs g{};
+    g.w0 = (const uint8_t*)blocks;
+    g.tables = (const uint8_t*)tables;
+    g.a = a;
+    g.tile_expert = tile_expert;
+    g.out = out;
+    g.experts = (int)experts, g.rows = (int)rows, g.cols = (int)cols, g.rbytes = (int)row_bytes(kind, cols);
+    g.n_tiles = (int)n_tiles;
+    return with_half_dtype(a_dtype, [&](auto* tp) {
+      using XT = std::remove_pointer_t<decltype(tp)>;
+      return kind == IQ3_S ? launch_stream<IQ3_S, XT, TS_PLAIN>(g, (hipStream_t)stream, "tile_matmul")
+                           : launch_stream<Q2_0, XT, TS_PLAIN>(g, (hipStream_t)stream, "tile_matmul");
+    });
+  }
   return with_kind(kind, [&](auto kc) {
     constexpr int K = decltype(kc)::value;
     return with_half_dtype(a_dtype, [&](auto* tp) {
@@ -219,6 +612,67 @@ int sh_tile_matmul(int kind, const void* blocks, const void* tables, int64_t exp
       return launch_tiles<K, XT>((const uint8_t*)blocks, (const uint8_t*)tables, experts, rows, cols, (const XT*)a,
                                  n_tiles, tile_expert, out, (hipStream_t)stream);
     });
+  });
+}
+
+}  // extern "C"
+
+extern "C" {
+
+int sh_tile_glu(int kind, const void* gate, const void* up, const void* tables, int64_t experts, int64_t rows,
+                int64_t cols, const void* x, int x_dtype, int64_t tokens, const int32_t* token, int64_t slots,
+                const int32_t* tile_expert, void* h, void* stream) {
+  int st = check_rows(kind, rows, cols, "tile_glu");
+  if (st) return st;
+  if (slots <= 0) return OK;
+  if (kind != IQ3_S && kind != Q2_0) return fail(E_UNSUPPORTED, "tile_glu: kind %d (Q2_0 or IQ3_S)", kind);
+  if (rows % (TS_RBV / 2) || cols % TS_KCH)
+    return fail(E_UNSUPPORTED, "tile_glu: %lld x %lld is not in blocks of %d x %d", (long long)rows, (long long)cols,
+                TS_RBV / 2, TS_KCH);
+  if (slots % TILE_TOKENS) return fail(E_SHAPE, "tile_glu: %lld slots are not whole tiles of 16", (long long)slots);
+  if (slots / TILE_TOKENS > (1 << 26) || tokens <= 0)
+    return fail(E_SHAPE, "tile_glu: %lld slots of %lld tokens", (long long)slots, (long long)tokens);
+  if (!gate || !up || (kind == IQ3_S && !tables) || !x || !token || !tile_expert || !h)
+    return fail(E_ARG, "tile_glu: null pointer");
+  if (((uintptr_t)x & 15) || ((uintptr_t)gate & 15) || ((uintptr_t)up & 15))
+    return fail(E_ARG, "tile_glu: activations and blocks must be 16-byte aligned");
+  TileStreamArgs g{};
+  g.w0 = (const uint8_t*)gate, g.w1 = (const uint8_t*)up, g.tables = (const uint8_t*)tables;
+  g.a = x, g.token = token, g.tile_expert = tile_expert, g.out = h;
+  g.experts = (int)experts, g.rows = (int)rows, g.cols = (int)cols, g.rbytes = (int)row_bytes(kind, cols);
+  g.n_tiles = (int)(slots / TILE_TOKENS), g.n_src = tokens;
+  return with_half_dtype(x_dtype, [&](auto* tp) {
+    using XT = std::remove_pointer_t<decltype(tp)>;
+    return kind == IQ3_S ? launch_stream<IQ3_S, XT, TS_GLU>(g, (hipStream_t)stream, "tile_glu")
+                         : launch_stream<Q2_0, XT, TS_GLU>(g, (hipStream_t)stream, "tile_glu");
+  });
+}
+
+int sh_tile_down(int kind, const void* down, const void* tables, int64_t experts, int64_t rows, int64_t cols,
+                 const void* h, int h_dtype, int64_t slots, const int32_t* tile_expert, const int32_t* pair,
+                 int64_t pairs, void* out, void* stream) {
+  int st = check_rows(kind, rows, cols, "tile_down");
+  if (st) return st;
+  if (slots <= 0 || pairs <= 0) return OK;
+  if (kind != IQ3_S && kind != Q2_0) return fail(E_UNSUPPORTED, "tile_down: kind %d (Q2_0 or IQ3_S)", kind);
+  if (rows % TS_RBV || cols % TS_KCH)
+    return fail(E_UNSUPPORTED, "tile_down: %lld x %lld is not in blocks of %d x %d", (long long)rows,
+                (long long)cols, TS_RBV, TS_KCH);
+  if (slots % TILE_TOKENS) return fail(E_SHAPE, "tile_down: %lld slots are not whole tiles of 16", (long long)slots);
+  if (slots / TILE_TOKENS > (1 << 26)) return fail(E_SHAPE, "tile_down: %lld slots", (long long)slots);
+  if (!down || (kind == IQ3_S && !tables) || !h || !tile_expert || !pair || !out)
+    return fail(E_ARG, "tile_down: null pointer");
+  if (((uintptr_t)h & 15) || ((uintptr_t)down & 15))
+    return fail(E_ARG, "tile_down: activations and blocks must be 16-byte aligned");
+  TileStreamArgs g{};
+  g.w0 = (const uint8_t*)down, g.tables = (const uint8_t*)tables;
+  g.a = h, g.pair = pair, g.tile_expert = tile_expert, g.out = out;
+  g.experts = (int)experts, g.rows = (int)rows, g.cols = (int)cols, g.rbytes = (int)row_bytes(kind, cols);
+  g.n_tiles = (int)(slots / TILE_TOKENS), g.n_src = pairs;
+  return with_half_dtype(h_dtype, [&](auto* tp) {
+    using XT = std::remove_pointer_t<decltype(tp)>;
+    return kind == IQ3_S ? launch_stream<IQ3_S, XT, TS_DOWN>(g, (hipStream_t)stream, "tile_down")
+                         : launch_stream<Q2_0, XT, TS_DOWN>(g, (hipStream_t)stream, "tile_down");
   });
 }
 

@@ -46,6 +46,9 @@ PROTOTYPES = {
     "sh_moe_decode_phase": [c_int, c_int, c_int, c_vp, c_vp, c_vp, c_i64, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_int,
                             c_vp, c_int, c_i64, c_i64, c_i64, c_i64, c_vp, c_vp, c_sz, c_vp],
     "sh_tile_matmul": [c_int, c_vp, c_vp, c_i64, c_i64, c_i64, c_vp, c_int, c_i64, c_vp, c_vp, c_vp],
+    "sh_tile_glu": [c_int, c_vp, c_vp, c_vp, c_i64, c_i64, c_i64, c_vp, c_int, c_i64, c_vp, c_i64, c_vp, c_vp,
+                    c_vp],
+    "sh_tile_down": [c_int, c_vp, c_vp, c_i64, c_i64, c_i64, c_vp, c_int, c_i64, c_vp, c_vp, c_i64, c_vp, c_vp],
     "sh_paged_attn_workspace": [c_i64, c_i64, c_i64, c_i64, c_i64],
     "sh_paged_attn": [c_vp, c_vp, c_vp, c_vp, c_i64, c_i64, c_i64, c_i64, c_i64, c_i64, ctypes.c_float, c_int, c_vp,
                       c_vp, c_sz, c_vp],

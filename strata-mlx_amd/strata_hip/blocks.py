@@ -325,12 +325,18 @@ def _lookup_glu(x, indices, up, gate, down):
 
 def tileable(kind: str, rows: int, cols: int) -> bool:
     """Whether `tile_matmul` takes a stack of such layers (strata_mlx/blocks.py:511-513): the reference's rule
-    (rows % 64, cols % 64, whole blocks), with columns in whole chunks of 256 and a row group of 64 rows that fits
-    in LDS beside the chunk buffers."""
-    rb = row_bytes(kind, cols) if cols % BLOCK[kind][0] == 0 else 0
-    room = 160 * 1024 - 2 * 64 * 256 * 2 - (32 * 1024 if kind == "IQ3_S" else 0 if kind in ("Q2_0", "Q3_K") else 16512)
-    return (rows % ROWS_TILE == 0 and cols % COLS_TILE == 0 and cols % BLOCK[kind][0] == 0 and cols % 256 == 0
-            and 64 * rb <= room)
+    (rows % 64, cols % 64, whole blocks), with columns in whole chunks of 256. Q2_0 and IQ3_S stream their rows
+    through LDS chunk by chunk; the other kinds keep a row group of 64 rows in LDS beside the chunk buffers."""
+    if rows % ROWS_TILE or cols % COLS_TILE or cols % BLOCK[kind][0] or cols % 256:
+        return False
+    if kind in STREAMED:
+        return True
+    rb = row_bytes(kind, cols)
+    room = 160 * 1024 - 2 * 64 * 256 * 2 - (0 if kind == "Q3_K" else 16512)
+    return 64 * rb <= room
+
+
+STREAMED = ("Q2_0", "IQ3_S")  # kinds with the fused gate / up / SwiGLU and down products of the prompt path
 
 
 def tiles_of(indices: torch.Tensor, experts: int) -> tuple:
@@ -354,9 +360,12 @@ def tiles_of(indices: torch.Tensor, experts: int) -> tuple:
 
 
 def tile_matmul(blocks: torch.Tensor, kind: str, shape: tuple, a: torch.Tensor, tile_expert: torch.Tensor) -> torch.Tensor:
-    """out[p] = W[expert of p's tile] . a[p] for a stack of `shape` (experts, rows, cols); a (P, cols) float16,
-    bfloat16 or float32, P a multiple of TOKENS_TILE; the weights rounded to a's type, float32 sums. Rows of a
-    tile naming no expert are left as they were (strata_mlx/blocks.py:516-536). Returns (P, rows) float32."""
+    """out[p] = W[expert of p's tile] . a[p] for a stack of `shape` (experts, rows, cols); a (P, cols) float16 or
+    bfloat16, P a multiple of TOKENS_TILE; the weights rounded to a's type, float32 sums. Rows of a tile naming no
+    expert are left as they were (strata_mlx/blocks.py:516-536). Returns (P, rows) float32. The reference also
+    takes float32 activations; here they raise ValueError (switch_glu sends float32 prompts to the matvec)."""
+    if a.dtype not in (torch.float16, torch.bfloat16):
+        raise ValueError(f"tile_matmul: activations of {a.dtype} (float16 or bfloat16)")
     experts, rows, cols = shape
     if not tileable(kind, rows, cols):
         raise ValueError(f"tile_matmul: {kind} ({rows}, {cols}) is not tileable")
@@ -382,24 +391,74 @@ def swiglu(gate: torch.Tensor, up: torch.Tensor) -> torch.Tensor:
     return (gate * sig) * up
 
 
+def tile_glu(gate, up, x: torch.Tensor, token: torch.Tensor, tile_expert: torch.Tensor) -> torch.Tensor:
+    """silu(gate . x[token[s]]) * (up . x[token[s]]) for every slot s of the tiles, the weights rounded to x's type,
+    float32 sums, the result rounded to x's type: `_tiled_glu`'s first two products and its swiglu
+    (strata_mlx/blocks.py:570-574) in one pass over gate's and up's rows. x (tokens, cols) float16 / bfloat16;
+    token (16 * tiles,) int32 from tiles_of. Rows of tiles naming no expert are left as they were."""
+    experts, rows, cols = gate.num_experts, gate.output_dims, gate.input_dims
+    if gate.kind != up.kind or (up.num_experts, up.output_dims, up.input_dims) != (experts, rows, cols):
+        raise ValueError("tile_glu: gate and up of one shape and kind expected")
+    x = x.contiguous()
+    tok = token.to(torch.int32).contiguous()
+    te = tile_expert.to(torch.int32).contiguous()
+    slots = tok.numel()
+    if slots != TOKENS_TILE * te.numel() or x.dim() != 2 or x.shape[1] != cols:
+        raise ValueError(f"tile_glu: {te.numel()} tiles, {slots} slots, x {tuple(x.shape)} for rows of {cols}")
+    _on_gpu(gate.blocks, up.blocks, x, tok, te)
+    h = torch.empty((slots, rows), dtype=x.dtype, device=x.device)
+    _lib.call("sh_tile_glu", _kind(gate.kind), _u8(gate.blocks).data_ptr(), _u8(up.blocks).data_ptr(),
+              _tabs(gate.kind, x.device), experts, rows, cols, x.data_ptr(), _lib.dtype_code(x.dtype), x.shape[0],
+              tok.data_ptr(), slots, te.data_ptr(), h.data_ptr(), _lib.stream_of(x))
+    return h
+
+
+def tile_down(down, h: torch.Tensor, tile_expert: torch.Tensor, where: torch.Tensor) -> torch.Tensor:
+    """down . h[where[p]] for every pair p, the weights rounded to h's type, float32 sums, the result rounded to
+    h's type: `_tiled_glu`'s last product, its un-permutation and its cast (strata_mlx/blocks.py:575) in one pass.
+    h (16 * tiles, cols) from tile_glu; where (pairs,) from tiles_of. Returns (pairs, rows)."""
+    experts, rows, cols = down.num_experts, down.output_dims, down.input_dims
+    h = h.contiguous()
+    te = tile_expert.to(torch.int32).contiguous()
+    slots, pairs = h.shape[0], where.numel()
+    if slots != TOKENS_TILE * te.numel() or h.shape[1] != cols:
+        raise ValueError(f"tile_down: h {tuple(h.shape)} for {te.numel()} tiles of rows of {cols}")
+    _on_gpu(down.blocks, h, te, where)
+    pair = torch.full((slots,), -1, dtype=torch.int32, device=h.device)  # the pair of each slot, -1 for none
+    pair[where.long()] = torch.arange(pairs, dtype=torch.int32, device=h.device)
+    out = torch.empty((pairs, rows), dtype=h.dtype, device=h.device)
+    _lib.call("sh_tile_down", _kind(down.kind), _u8(down.blocks).data_ptr(), _tabs(down.kind, h.device), experts,
+              rows, cols, h.data_ptr(), _lib.dtype_code(h.dtype), slots, te.data_ptr(), pair.data_ptr(), pairs,
+              out.data_ptr(), _lib.stream_of(h))
+    return out
+
+
 def _tiled_glu(x, indices, up, gate, down):
-    """The three products of a prompt's pairs through `tile_matmul`, the pairs in tiles (blocks.py:566-576)."""
+    """The three products of a prompt's pairs through the tiles (strata_mlx/blocks.py:566-576):
+    h = swiglu(gate . a, up . a) rounded to x's type, out = (down . h)[where] rounded to x's type. Q2_0 and IQ3_S
+    in two fused passes (tile_glu, tile_down); other kinds through tile_matmul as the reference composes it."""
     tiles, token, where = tiles_of(indices, gate.num_experts)
-    a = x.reshape(-1, x.shape[-1])[token.long()]
+    x2 = x.reshape(-1, x.shape[-1])
+    if (gate.kind == up.kind == down.kind and gate.kind in STREAMED and x.dtype in (torch.float16, torch.bfloat16)
+            and gate.output_dims % 32 == 0):
+        out = tile_down(down, tile_glu(gate, up, x2, token, tiles), tiles, where)
+        return out.reshape(*indices.shape, down.output_dims)
+    a = x2[token.long()]
 
     def product(lin, a):
         return tile_matmul(lin.blocks, lin.kind, lin.shape, a, tiles)
 
-    h = swiglu(product(gate, a).to(x.dtype), product(up, a).to(x.dtype))
+    h = swiglu(product(gate, a), product(up, a)).to(x.dtype)
     out = product(down, h)[where.long()].to(x.dtype)
     return out.reshape(*indices.shape, down.output_dims)
 
 
 def switch_glu(x: torch.Tensor, indices: torch.Tensor, up, gate, down) -> torch.Tensor:
     """down(silu(gate(x)) * up(x)) through each token's experts: x (..., in), indices (..., experts per token)
-    (strata_mlx/blocks.py:801-829). The branches: a prompt's many pairs through the tiles; otherwise gate and up
-    by the expert matvec (one row of x to each token's k pairs) and down taking silu(gate) * up itself."""
-    if (indices.numel() >= TILES_FROM and x.dtype in (torch.float16, torch.bfloat16, torch.float32)
+    (strata_mlx/blocks.py:801-829). The branches: a prompt's many pairs through the tiles (float16 / bfloat16;
+    the reference also tiles float32, which here takes the matvec); otherwise gate and up by the expert matvec
+    (one row of x to each token's k pairs) and down taking silu(gate) * up itself."""
+    if (indices.numel() >= TILES_FROM and x.dtype in (torch.float16, torch.bfloat16)
             and all(tileable(lin.kind, lin.output_dims, lin.input_dims) for lin in (up, gate, down))):
         return _tiled_glu(x, indices, up, gate, down)
     if indices.numel() >= LOOKUP_FROM and all(lookable(lin, x.dtype) for lin in (up, gate, down)):

@@ -69,3 +69,82 @@ def test_a_prompt_in_tiles_of_skewed_routing(kind, tables, dev):
         pairs = np.nonzero(flat == e)[0]
         want[pairs] = xs[pairs // K] @ wr[e].T
     assert np.abs(got - want).max() <= 2e-6 * np.abs(want).max()
+
+
+@pytest.mark.parametrize("kind", ["IQ3_S", "Q2_0"])
+def test_long_runs_and_gaps_of_tiles(kind, tables, dev):
+    """Runs of one expert longer than a unit of eight tiles, a run broken by a tile naming no expert, a run at the
+    end: every real tile's rows against the oracle, the others left as they were."""
+    shape = (3, 128, 512)
+    raw, w, rng = stack(kind, *shape, 4, tables)
+    tiles = np.array([0] * 19 + [3] + [0] * 3 + [2, 1, 1] + [7] * 2 + [1] * 9, dtype=np.int32)
+    a = torch.from_numpy(rng.standard_normal((16 * len(tiles), shape[2])).astype(np.float32)).to(torch.bfloat16)
+    got = SB.tile_matmul(torch.from_numpy(raw).to(dev), kind, shape, a.to(dev), torch.from_numpy(tiles).to(dev))
+    want = OT.tile_matmul(w, a.float().numpy(), tiles, "bfloat16")
+    real = ~np.isnan(want)
+    assert real.any() and np.abs(got.cpu().numpy()[real] - want[real]).max() <= 2e-6 * np.abs(want[real]).max()
+
+
+def prompt_want(wg, wu, wd, x, idx, dtype):
+    """The reference's composition (strata_mlx/blocks.py:566-576) in float64 from the rounded weights: h =
+    swiglu(gate . a, up . a) rounded to x's type, out = down . h rounded to x's type; pair by pair."""
+    K = idx.shape[-1]
+    flat, xs = idx.reshape(-1), x.float().numpy().astype(np.float64)
+    r = {n: OR.round_to(m, dtype).astype(np.float64) for n, m in (("g", wg), ("u", wu), ("d", wd))}
+    out = np.zeros((flat.size, wd.shape[1]))
+    hs = np.zeros((flat.size, wg.shape[1]), dtype=np.float32)
+    for e in np.unique(flat):
+        pairs = np.nonzero(flat == e)[0]
+        a = xs[pairs // K]
+        g, u = a @ r["g"][e].T, a @ r["u"][e].T
+        with np.errstate(over="ignore"):
+            h = OR.round_to((g / (1.0 + np.exp(-g)) * u).astype(np.float32), dtype)
+        hs[pairs] = h
+        out[pairs] = h.astype(np.float64) @ r["d"][e].T
+    return out, hs
+
+
+@pytest.mark.parametrize("kind,dtype,T,E", [("IQ3_S", torch.bfloat16, 256, 64), ("Q2_0", torch.float16, 256, 64),
+                                           ("IQ3_S", torch.bfloat16, 4096, 64)])
+def test_the_prompt_layer_through_the_fused_products(kind, dtype, T, E, tables, dev):
+    """switch_glu's prompt branch (gate / up / SwiGLU in one pass, down and the un-permutation in another) against
+    the reference's composition pair by pair: Zipf(1.1) routing, top-10; 4096 tokens make more than one window
+    of 2048 tiles. Within 1e-2 of the largest output (bfloat16 / float16), most much closer."""
+    F, D, K = 256, 512, 10
+    rng = np.random.default_rng(6)
+    raws, ws = {}, {}
+    for n, (r, c) in (("g", (F, D)), ("u", (F, D)), ("d", (D, F))):
+        raws[n], ws[n], _ = stack(kind, E, r, c, 7 + len(raws), tables)
+    lin = {n: SB.BlockSwitchLinear(torch.from_numpy(raws[n]).to(dev), kind, (E,) + ws[n].shape[1:]) for n in raws}
+    logits = synth.zipf_logits(rng, T, E)
+    idx = OR.top_k(logits.float().numpy(), K)
+    x = torch.from_numpy(rng.standard_normal((T, D)).astype(np.float32)).to(dtype)
+    got = SB.BlockSwitchGLU(lin["g"], lin["u"], lin["d"])(x.to(dev), torch.from_numpy(idx).to(dev))
+    assert got.shape == (T, K, D) and got.dtype == dtype
+    want, _ = prompt_want(ws["g"], ws["u"], ws["d"], x, idx, NAME[dtype])
+    err = np.abs(got.float().cpu().numpy().reshape(-1, D) - want)
+    scale = np.abs(want).max()
+    assert err.max() <= 1e-2 * scale
+    assert np.median(err) <= 2e-3 * scale
+
+
+def test_the_fused_gate_up_is_swiglu_of_the_tile_products(tables, dev):
+    """tile_glu against tile_matmul's two products and the reference's swiglu order (float32 swiglu, then
+    rounded): equal but for the last bit of the rounding."""
+    kind, E, F, D, T, K = "IQ3_S", 16, 128, 512, 64, 4
+    rng = np.random.default_rng(8)
+    raws = {n: synth.random_blocks(kind, E * F, D, rng) for n in ("g", "u")}
+    lin = {n: SB.BlockSwitchLinear(torch.from_numpy(raws[n]).to(dev), kind, (E, F, D)) for n in raws}
+    idx = torch.from_numpy(rng.integers(0, E, (T, K)).astype(np.int32)).to(dev)
+    x = torch.from_numpy(rng.standard_normal((T, D)).astype(np.float32)).to(torch.bfloat16).to(dev)
+    te, token, where = SB.tiles_of(idx, E)
+    h = SB.tile_glu(lin["g"], lin["u"], x, token, te)
+    a = x[token.long()]
+    g = SB.tile_matmul(lin["g"].blocks, kind, (E, F, D), a, te)
+    u = SB.tile_matmul(lin["u"].blocks, kind, (E, F, D), a, te)
+    want = (torch.nn.functional.silu(g) * u).to(torch.bfloat16)
+    real = torch.zeros(h.shape[0], dtype=torch.bool, device=dev)
+    real[where.long()] = True
+    diff = (h[real].float() - want[real].float()).abs()
+    assert diff.max().item() <= 2 ** -7 * want[real].float().abs().max().item()
+    assert (diff == 0).float().mean().item() > 0.99
