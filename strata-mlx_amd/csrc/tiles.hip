@@ -22,6 +22,13 @@ constexpr int TILE_TOKENS = 16, TG = 8, RB = 64, KCH = 256;
 // stage_tables lays them out
 template <int KIND> constexpr int tile_tab_bytes() { return KIND == IQ3_S ? IQ3S_SIGNED_BYTES : (KIND == Q2_0 || KIND == Q3_K) ? 0 : LDS_TAB_MAX; }
 
+// two floats rounded to nearest even in XT, packed (lo in the low half): one v_cvt_pk a pair
+template <typename XT> __device__ __forceinline__ uint32_t pack_rne(float lo, float hi) {
+  typedef float f2 __attribute__((ext_vector_type(2)));
+  typedef XT x2 __attribute__((ext_vector_type(2)));
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f2){lo, hi}, x2));
+}
+
 // run `n` (32 weights) of a row of blocks in LDS, dequantized and rounded to XT, as 16 XT values in 4 u32x4 each
 // (the run's weights 8c .. 8c + 7 in w[c])
 template <int KIND, typename XT>
@@ -60,9 +67,7 @@ __device__ __forceinline__ void dequant_run(const uint8_t* row, int n, const uin
   for (int c = 0; c < 4; ++c) {
     uint32_t p[4];
 #pragma unroll
-    for (int h = 0; h < 4; ++h)
-      p[h] = (uint32_t)__builtin_bit_cast(uint16_t, from_f32<XT>(f[8 * c + 2 * h])) |
-             ((uint32_t)__builtin_bit_cast(uint16_t, from_f32<XT>(f[8 * c + 2 * h + 1])) << 16);
+    for (int h = 0; h < 4; ++h) p[h] = pack_rne<XT>(f[8 * c + 2 * h], f[8 * c + 2 * h + 1]);
     w[c] = u32x4{p[0], p[1], p[2], p[3]};
   }
 }
@@ -385,57 +390,58 @@ __global__ __launch_bounds__(TS_NT) void k_tile_stream(TileStreamArgs g) {
     };
 
     if (wave < 8) {
-      // ---- producers: the ring and the dequantization; lane (row v, piece / run j). The lane's offsets are
-      // recomputed each step from an opaque copy of the thread index: hoisted out of the loop they would stay
-      // live through the consumers' loop as well and spill.
-      auto row_src = [&](const TsCursor& s, int v) {  // the first byte of row v's chunk
+      // ---- producers: the ring and the dequantization; lane (row v, piece / run j), the row's first byte in
+      // the item of each cursor recomputed only when the cursor enters an item
+      const int v = tid >> 3, j = tid & 7;
+      auto row_base = [&](const TsCursor& s) {
         const uint8_t* stack = g.w0;
         int r = s.rb * VR + v;
         if constexpr (MODE == TS_GLU) {
           stack = v < VR ? g.w0 : g.w1;
           r = s.rb * VR + (v & (VR - 1));
         }
-        return stack + ((int64_t)s.e * g.rows + r) * rbytes + (int64_t)s.c * CB;
+        return stack + ((int64_t)s.e * g.rows + r) * rbytes;
       };
-      auto issue = [&](const TsCursor& k) {  // chunk k.q into ring slot k.q % TS_NR: piece j of row v
-        const int t = opaque(tid), v = t >> 3, j = t & 7, q = k.q;
-        const uint8_t* src = row_src(k, v);
+      TsCursor ci = cur_at(0), cd = cur_at(0);  // the next chunk to load, the next to dequantize
+      const uint8_t* ibase = row_base(ci);
+      const uint8_t* dbase = ibase;
+      int islot = 0, dslot = 0;  // their ring slots
+      auto issue = [&]() {  // chunk ci.q into ring slot islot: piece j of row v
+        const uint8_t* src = ibase + ci.c * CB;
         const int lead = (int)((uintptr_t)src & 15);
-        if (16 * j < lead + CB)
-          lds_dma16p(src - lead + 16 * j, ring_lds + (uint32_t)((q % TS_NR) * TS_SLOT + wave * 1024));
+        if (16 * j < lead + CB) lds_dma16p(src - lead + 16 * j, ring_lds + (uint32_t)(islot * TS_SLOT + wave * 1024));
+        islot = islot + 1 == TS_NR ? 0 : islot + 1;
+        cur_next(ci);
+        if (ci.c == 0 && ci.q < Q) ibase = row_base(ci);
       };
-      auto dequant = [&](const TsCursor& k) {  // chunk k.q into buffer k.q & 1: run j of row v
-        const int t = opaque(tid), v = t >> 3, j = t & 7, q = k.q;
-        const uint8_t* src = row_src(k, v);
-        const uint8_t* raw = ring + (q % TS_NR) * TS_SLOT + v * (TS_PPR * 16) + ((uintptr_t)src & 15);
+      auto dequant = [&]() {  // chunk cd.q into buffer cd.q & 1: run j of row v
+        const uint8_t* src = dbase + cd.c * CB;
+        const uint8_t* raw = ring + dslot * TS_SLOT + v * (TS_PPR * 16) + ((uintptr_t)src & 15);
         u32x4 w[4];
         dequant_run<KIND, XT>(raw, j, tab, w);
-        XT* dst = wl + (q & 1) * TS_BUF + v * TS_KCH;
+        XT* dst = wl + (cd.q & 1) * TS_BUF + v * TS_KCH;
 #pragma unroll
         for (int h = 0; h < 4; ++h) *(u32x4*)(dst + 8 * ((4 * j + h) ^ (v & 15))) = w[h];
+        dslot = dslot + 1 == TS_NR ? 0 : dslot + 1;
+        cur_next(cd);
+        if (cd.c == 0 && cd.q < Q) dbase = row_base(cd);
       };
       const int lead0 = min(TS_LEAD, Q);
-      TsCursor ci = cur_at(0), cd = cur_at(0);  // the next chunk to load, the next to dequantize
-      for (int q = 0; q < lead0; ++q) {
-        issue(ci);
-        cur_next(ci);
-      }
+      for (int q = 0; q < lead0; ++q) issue();
       if constexpr (KIND == IQ3_S) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // (the table, and the lead)
       wait_vmcnt(lead0 - 1);
       lds_sync();
-      dequant(cd);
-      cur_next(cd);
+      dequant();
       for (int q = 0; q < Q; ++q) {
-        if (ci.q < Q) {  // ci.q == q + TS_LEAD
-          issue(ci);
-          cur_next(ci);
+        if (ci.q < Q) {  // ci.q == q + TS_LEAD: the steady state, TS_LEAD - 1 loads after chunk q + 1's
+          issue();
+          static_assert(TS_LEAD - 1 == 4, "the immediate below");
+          asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
+        } else if (q + 1 < Q) {
+          wait_vmcnt(Q - 1 - (q + 1));
         }
-        if (q + 1 < Q) wait_vmcnt(max(0, min(q + TS_LEAD, Q - 1) - (q + 1)));
         lds_sync();
-        if (cd.q < Q) {  // cd.q == q + 1
-          dequant(cd);
-          cur_next(cd);
-        }
+        if (cd.q < Q) dequant();  // cd.q == q + 1
       }
     } else {
       // ---- consumers: the 64 rows (four fragments of 16) against tile cw of the unit; the fragments of
@@ -443,20 +449,40 @@ __global__ __launch_bounds__(TS_NT) void k_tile_stream(TileStreamArgs g) {
       const int cw = wave - 8;
       const XT* a = (const XT*)g.a;
       f32x4 acc[4];
+      int pr[4] = {0, 0, 0, 0};  // TS_DOWN: the output rows of the lane's four slots in the current item
       u32x4 af[2][TS_KCH / 32];
       const XT* arow = a;
 #pragma unroll
       for (int f = 0; f < 4; ++f) acc[f] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+      TsCursor cs = cur_at(0), cl = cur_at(0);  // the chunk to multiply, the next to load fragments of
+      // TS_GLU: the token of the lane's slot in the item the loading cursor enters next, loaded an item ahead
+      auto item_after = [&](TsCursor k) {  // chunk 0 of the item after k's (k at a chunk 0)
+        k.q += nch;
+        k.rb += gmod;
+        k.u += gdiv;
+        if (k.rb >= rblk) k.rb -= rblk, ++k.u;
+        if (k.q < Q) cur_fill(k);
+        return k;
+      };
+      auto token_of = [&](const TsCursor& k) {
+        int t = 0;
+        if (k.q < Q && cw < k.len) t = g.token[(int64_t)(k.start + cw) * TILE_TOKENS + (lane & 15)];
+        return t;
+      };
+      int tok_next = 0;
+      if constexpr (MODE == TS_GLU) tok_next = token_of(cl);
       auto load_a = [&](const TsCursor& s, auto bc) {  // chunk s.q's fragments of the lane's row into af[bc]
         constexpr int BUF = decltype(bc)::value;
         const int ln = opaque(lane), n = ln & 15, gq = ln >> 4;
-        if (cw < s.len) {
-          if (s.c == 0) {  // a new item: the row of the lane's slot
-            const int64_t slot = (int64_t)(s.start + cw) * TILE_TOKENS + n;
-            int64_t row = slot;
-            if constexpr (MODE == TS_GLU) row = min(max((int64_t)g.token[slot], (int64_t)0), g.n_src - 1);
-            arow = a + row * g.cols;
+        if (s.c == 0) {  // a new item: the row of the lane's slot
+          int64_t row = (int64_t)(s.start + cw) * TILE_TOKENS + n;
+          if constexpr (MODE == TS_GLU) {
+            row = min(max((int64_t)tok_next, (int64_t)0), g.n_src - 1);
+            tok_next = token_of(item_after(s));
           }
+          arow = a + row * g.cols;
+        }
+        if (cw < s.len) {
 #pragma unroll
           for (int ks = 0; ks < TS_KCH / 32; ++ks)
             af[BUF][ks] = *(const u32x4*)(arow + s.c * TS_KCH + ks * 32 + 8 * gq);
@@ -465,7 +491,6 @@ __global__ __launch_bounds__(TS_NT) void k_tile_stream(TileStreamArgs g) {
           for (int ks = 0; ks < TS_KCH / 32; ++ks) af[BUF][ks] = u32x4{0u, 0u, 0u, 0u};
         }
       };
-      TsCursor cs = cur_at(0), cl = cur_at(0);  // the chunk to multiply, the next to load fragments of
       auto step = [&](auto bc) {
         constexpr int BUF = decltype(bc)::value;
         const TsCursor& s = cs;
@@ -473,27 +498,31 @@ __global__ __launch_bounds__(TS_NT) void k_tile_stream(TileStreamArgs g) {
         lds_sync();
         const XT* wb = wl + (q & 1) * TS_BUF;
         if (cw < s.len) {
-          const int ln = opaque(lane), n = ln & 15;
-#pragma unroll
-          for (int ks = 0; ks < TS_KCH / 32; ++ks) {
-            const int gq = ln >> 4;
-            u32x4 b[4];
+          const int ln = opaque(lane), n = ln & 15, gq = ln >> 4;
+          auto read_b = [&](int ks, u32x4* b) {
 #pragma unroll
             for (int f = 0; f < 4; ++f) {
               const int r = 16 * f + n;
               b[f] = *(const u32x4*)(wb + r * TS_KCH + 8 * ((4 * ks + gq) ^ (r & 15)));
             }
+          };
+          u32x4 b[2][4];  // the fragments of k-step ks + 1 are read while those of ks multiply
+          read_b(0, b[0]);
 #pragma unroll
-            for (int f = 0; f < 4; ++f) acc[f] = mfma<XT>(af[BUF][ks], b[f], acc[f]);
+          for (int ks = 0; ks < TS_KCH / 32; ++ks) {
+            if (ks + 1 < TS_KCH / 32) read_b(ks + 1, b[(ks + 1) & 1]);
+            __builtin_amdgcn_sched_barrier(0);  // (the scheduler would sink the reads to their MFMAs)
+#pragma unroll
+            for (int f = 0; f < 4; ++f) acc[f] = mfma<XT>(af[BUF][ks], b[ks & 1][f], acc[f]);
           }
-          if (s.c == nch - 1) {  // the item's rows are done
-            const int gq = ln >> 4;
-            const int64_t slot0 = (int64_t)(s.start + cw) * TILE_TOKENS + 4 * gq;
-            int pr[4] = {0, 0, 0, 0};  // TS_DOWN: the slots' output rows, loaded before any store
-            if constexpr (MODE == TS_DOWN) {
+          const int64_t slot0 = (int64_t)(s.start + cw) * TILE_TOKENS + 4 * gq;
+          if constexpr (MODE == TS_DOWN) {  // the slots' output rows, at the item's first chunk
+            if (s.c == 0) {
 #pragma unroll
               for (int i = 0; i < 4; ++i) pr[i] = g.pair[slot0 + i];
             }
+          }
+          if (s.c == nch - 1) {  // the item's rows are done
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
               if constexpr (MODE == TS_PLAIN) {
