@@ -54,6 +54,8 @@ template <typename XT> __device__ __forceinline__ f32x4 mfma16x16x16(uint32_t a0
     return __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(h4, a), __builtin_bit_cast(h4, b), c, 0, 0, 0);
 }
 
+typedef short v4i16 __attribute__((ext_vector_type(4)));
+
 template <typename XT> __device__ __forceinline__ uint32_t pack_pair(float lo, float hi) {
   return (uint32_t)__builtin_bit_cast(uint16_t, from_f32<XT>(lo)) |
          ((uint32_t)__builtin_bit_cast(uint16_t, from_f32<XT>(hi)) << 16);
@@ -192,12 +194,18 @@ __global__ __launch_bounds__(ATT_NT) void k_attn_split(AttnArgs a) {
           for (int i = 0; i < 4; ++i) O[dt][i] *= ar[i];
       }
       const uint32_t pa0 = pack_pair<XT>(p[0], p[1]), pa1 = pack_pair<XT>(p[2], p[3]);
+      // V fragments by transposing LDS reads: within each 16-lane group, lane i receives element i % 4 of the
+      // 8-byte pieces named by lanes i / 4 + 4m (m = 0..3). Lane (g, n) names row 4g + n / 4, dims
+      // 16 dt + 4 (n % 4) .. + 3, so it receives V[4g + m][16 dt + n], m = 0..3: the B operand of O += P V.
+      const int vr = 4 * g + (n >> 2), vq = n & 3;
 #pragma unroll
       for (int dt = 0; dt < NDT; ++dt) {
-        const int cv = 2 * dt + (n >> 3), e2 = (n & 7) * 2;  // the chunk and byte of dim 16 dt + n
-        auto vat = [&](int r) { return (uint32_t) * (const uint16_t*)(vt + r * RS + 16 * (cv ^ (r & 15)) + e2); };
-        const uint32_t v0 = vat(4 * g), v1 = vat(4 * g + 1), v2 = vat(4 * g + 2), v3 = vat(4 * g + 3);
-        O[dt] = mfma16x16x16<XT>(pa0, pa1, v0 | (v1 << 16), v2 | (v3 << 16), O[dt]);
+        const int cv = 2 * dt + (vq >> 1);  // the 16-byte chunk of dims 16 dt + 4 vq
+        const uint8_t* vp = vt + vr * RS + 16 * (cv ^ (vr & 15)) + 8 * (vq & 1);
+        const v4i16 vv = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) v4i16*)vp);
+        const uint32_t b0 = (uint32_t)(uint16_t)vv[0] | ((uint32_t)(uint16_t)vv[1] << 16);
+        const uint32_t b1 = (uint32_t)(uint16_t)vv[2] | ((uint32_t)(uint16_t)vv[3] << 16);
+        O[dt] = mfma16x16x16<XT>(pa0, pa1, b0, b1, O[dt]);
       }
     }
     lds_sync();  // every wave is done with this step's buffer before the step after next fills it
