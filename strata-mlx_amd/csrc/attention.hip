@@ -64,7 +64,7 @@ template <typename XT> __device__ __forceinline__ uint32_t pack_pair(float lo, f
 // Block: 4 waves; RT4 row tiles of 16 rows (1, 2 or 4) x PL = 4 / RT4 tile phases. A step stages PL tiles; wave
 // (rt, ph) multiplies row tile rt against the step's tile ph.
 template <typename XT, int D, bool CELLS>
-__global__ __launch_bounds__(ATT_NT) void k_attn_split(AttnArgs a) {
+__global__ __launch_bounds__(ATT_NT, 3) void k_attn_split(AttnArgs a) {  // (3 blocks a CU by registers)
   constexpr int NC = D / 32, NDT = D / 16, PI = att_part_insts<D>(), NCH = D / 8;  // NCH: chunks a row
   constexpr int PB = att_part_bytes<D>(), RS = D * 2;  // bytes a staged row
   extern __shared__ u32x4 dyn[];
@@ -352,12 +352,21 @@ template <int D, bool CELLS> static size_t attn_lds(int rows_here, int tiles_per
 // quarter of its K and V (16 positions x D x 2 x 2 bytes a tile)
 static int att_min_tiles(int rows) { return std::max(att_phases(std::min(64, rows)), (std::min(64, rows) + 7) / 8); }
 
-// blocks a CU by LDS (the stage and the phase merge; the tables taken at 4 KiB)
+// blocks a CU by LDS (the stage and the phase merge; the tables taken at 4 KiB) and by registers (the split
+// kernel's occupancy at that LDS, asked of the runtime for one representative instantiation a head size, so that
+// workspace sizing and launch plan alike)
 static int att_blocks_per_cu(int rows_here, int D) {
   const int PL = att_phases(rows_here);
   const size_t stage = 2 * (size_t)(2 * PL * 16 * D * 2) + 4096;
   const size_t merge = PL > 1 ? sizeof(float) * (2 * ATT_WAVES * 64 + (size_t)ATT_WAVES * D * 16) : 0;
-  return (int)std::max<size_t>(1, std::min<size_t>(8, 160 * 1024 / std::max(stage, merge)));
+  const size_t lds = std::max(stage, merge);
+  int by_regs = 0;
+  const hipError_t e = D == 256 ? hipOccupancyMaxActiveBlocksPerMultiprocessor(&by_regs, k_attn_split<bf16, 256, false>,
+                                                                             ATT_NT, lds)
+                                : hipOccupancyMaxActiveBlocksPerMultiprocessor(&by_regs, k_attn_split<bf16, 128, false>,
+                                                                             ATT_NT, lds);
+  if (e != hipSuccess || by_regs < 1) by_regs = 1;
+  return (int)std::max<size_t>(1, std::min<size_t>({8, 160 * 1024 / lds, (size_t)by_regs}));
 }
 
 template <typename XT, int D, bool CELLS> static int launch_attn(AttnArgs a, hipStream_t stream) {
