@@ -40,9 +40,11 @@ __global__ __launch_bounds__(NWMAX * 64) void k_stack_mv(const uint8_t* __restri
   extern __shared__ u32x4 dyn[];
   uint8_t* lds = (uint8_t*)dyn;
   const uint32_t lds_base = SH_LDS_ADDR(dyn);
-  // [2][kw - 1][rg][64][TPG]: the column splits' partial sums of the last two items (read a barrier later)
+  // [2][kw - 1][rg][64][TPG] (RW 2: the splits after the first; the first's wave adds them to its own) or
+  // [2][kw][rg][64][TPG] (RW 1: every split; the entries' sums shared out over all waves): the column splits'
+  // partial sums of the last two items, read a barrier later
   float* red = (float*)(lds + P.red_off);
-  const int red_sz = (P.kw - 1) * P.rg * 64 * TPG;
+  const int red_sz = (RW == 1 ? P.kw : P.kw - 1) * P.rg * 64 * TPG;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   // RW 1: wave (r, h) multiplies row group r over column split h; RW 2: wave h both row groups over split h (one
@@ -105,8 +107,21 @@ __global__ __launch_bounds__(NWMAX * 64) void k_stack_mv(const uint8_t* __restri
 #pragma unroll
   for (int r = 0; r < RW; ++r) pend_at[r] = -1;
   int pend_buf = 0;
+  int fin_m = -1, fin_r0 = 0;  // RW 1: the item whose results are pending, its matrix and first row
   auto finish = [&]() {
     const float* rb = red + pend_buf * red_sz;
+    if constexpr (RW == 1) {  // entry e = (row group, lane, token slot) of the item's rg x 64 x TPG: thread e's
+      if (fin_m < 0) return;
+      const int entries = P.rg * 64 * TPG;
+      for (int e = threadIdx.x; e < entries; e += nt) {
+        const int t = e % TPG, l = (e / TPG) & 63, r = e / (64 * TPG);
+        const int row = fin_r0 + r * 16 + (l & 15), tok = (l >> 4) * TPG + t;
+        float total = rb[e];
+        for (int k2 = 1; k2 < P.kw; ++k2) total += rb[k2 * entries + e];
+        if (tok < P.tokens && row < P.rows) out[((int64_t)fin_m * P.tokens + tok) * P.rows + row] = from_f32<XT>(total);
+      }
+      return;
+    }
     const int g = lane >> 4;
 #pragma unroll
     for (int r = 0; r < RW; ++r) {
@@ -147,12 +162,17 @@ __global__ __launch_bounds__(NWMAX * 64) void k_stack_mv(const uint8_t* __restri
       if ((rg0 + r) * 16 < rows_here)
         item_mac<KIND, MT, TPG, GPER>(row0 + (size_t)(rg0 + r) * 16 * P.rstride + wcol, P.rstride, X,
                                       (const uint32_t*)lds, kr, acc[r]);
-    if (kh > 0) {
+    if (RW == 1 || kh > 0) {
+      const int k0 = RW == 1 ? kh : kh - 1;
 #pragma unroll
       for (int r = 0; r < RW; ++r)
 #pragma unroll
         for (int t = 0; t < TPG; ++t)
-          red[(item & 1) * red_sz + (((kh - 1) * P.rg + rg0 + r) * 64 + lane) * TPG + t] = acc[r][t];
+          red[(item & 1) * red_sz + ((k0 * P.rg + rg0 + r) * 64 + lane) * TPG + t] = acc[r][t];
+    }
+    if constexpr (RW == 1) {
+      fin_m = m, fin_r0 = r0, pend_buf = item & 1;
+      continue;
     }
 #pragma unroll
     for (int r = 0; r < RW; ++r) {
@@ -194,7 +214,7 @@ static int launch_stack(const uint8_t* blocks, const uint8_t* tables, int64_t n_
     return fail(E_UNSUPPORTED, "stack_matvec: rows of %lld bytes", (long long)P.rbytes);
   P.buf_bytes = P.loads * 16 * nt;
   P.ring_off = KIND == IQ3_S ? IQ3S_SIGNED_BYTES : 0;
-  const size_t red = (size_t)2 * (P.kw - 1) * P.rg * 64 * TPG * 4, tail = 128;
+  const size_t red = (size_t)2 * (RW == 1 ? P.kw : P.kw - 1) * P.rg * 64 * TPG * 4, tail = 128;
   const size_t cap = 160 * 1024;
   // direct loads into LDS land below 128 KiB: the table and the ring stay under it
   const size_t dma_limit = 128 * 1024;
