@@ -121,8 +121,7 @@ __global__ __launch_bounds__(256) void k_moe_combine(const XT* __restrict__ y, c
 }
 
 // ---- tiles_of (strata_mlx/blocks.py:539-563): the pairs of a prompt chunk in tiles of 16 slots, each tile one
-// expert's; pairs of an expert keep their order. Two kernels: the count of each expert, then one block an expert
-// (and one more for the tiles no pair fills).
+// expert's; pairs of an expert keep their order. Two kernels: the count of each expert, then the placement.
 constexpr int TOKENS_TILE = 16;
 
 __global__ __launch_bounds__(1024) void k_tile_counts(const int32_t* __restrict__ flat, int pairs, int experts,
@@ -130,72 +129,102 @@ __global__ __launch_bounds__(1024) void k_tile_counts(const int32_t* __restrict_
   extern __shared__ int32_t c[];
   for (int e = threadIdx.x; e < experts; e += 1024) c[e] = 0;
   __syncthreads();
-  for (int p = threadIdx.x; p < pairs; p += 1024) {
-    int e = flat[p];
-    if (e >= 0 && e < experts) atomicAdd(&c[e], 1);
+  for (int p0 = threadIdx.x; p0 < pairs; p0 += 8 * 1024) {  // eight loads in flight a thread
+    int v[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = p0 + 1024 * i < pairs ? flat[p0 + 1024 * i] : -1;
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      if (v[i] >= 0 && v[i] < experts) atomicAdd(&c[v[i]], 1);
   }
   __syncthreads();
   for (int e = threadIdx.x; e < experts; e += 1024) counts[e] = c[e];
 }
 
-__global__ __launch_bounds__(256) void k_tile_place(const int32_t* __restrict__ flat, int pairs, int k, int experts,
-                                                    const int32_t* __restrict__ counts, int most,
-                                                    int32_t* __restrict__ tile_expert, int32_t* __restrict__ token,
-                                                    int32_t* __restrict__ where) {
-  __shared__ int32_t part[256];
-  __shared__ int32_t wave_n[4];
+// One block an expert (and one more for the tiles no pair fills), 16 waves. The pairs go by in batches of
+// 16 x 1024: wave w scans its run of 1024 consecutive pairs of the batch, 16 a lane, once into bit masks of the
+// pairs that are this expert's; their counts, summed over the earlier waves, place each wave's run; the masks'
+// ballots rank the pairs within it. Pairs of the expert keep their order.
+constexpr int PLACE_NT = 1024, PLACE_PER = 16;
+
+__device__ __forceinline__ int place_block_sum(int v, int32_t* s_w) {
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+#pragma unroll
+  for (int d = 32; d >= 1; d >>= 1) v += __shfl_xor(v, d);
+  if (lane == 0) s_w[wv] = v;
+  __syncthreads();
+  int total = 0;
+#pragma unroll
+  for (int w = 0; w < PLACE_NT / 64; ++w) total += s_w[w];
+  __syncthreads();
+  return total;
+}
+
+__global__ __launch_bounds__(PLACE_NT) void k_tile_place(const int32_t* __restrict__ flat, int pairs, int k,
+                                                         int experts, const int32_t* __restrict__ counts, int most,
+                                                         int32_t* __restrict__ tile_expert,
+                                                         int32_t* __restrict__ token, int32_t* __restrict__ where) {
+  __shared__ int32_t s_w[PLACE_NT / 64];
   const int e = blockIdx.x;
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const uint64_t below = (1ull << lane) - 1ull;
   // tiles of the experts before this one, and all tiles (the tail block needs the total)
   int before = 0, all = 0;
-  for (int j = tid; j < experts; j += 256) {
-    int t = (counts[j] + TOKENS_TILE - 1) / TOKENS_TILE;
+  for (int j = tid; j < experts; j += PLACE_NT) {
+    const int t = (counts[j] + TOKENS_TILE - 1) / TOKENS_TILE;
     all += t;
     if (j < e) before += t;
   }
-  part[tid] = before;
-  __syncthreads();
-  for (int s = 128; s > 0; s >>= 1) {
-    if (tid < s) part[tid] += part[tid + s];
-    __syncthreads();
-  }
-  before = part[0];
-  __syncthreads();
-  part[tid] = all;
-  __syncthreads();
-  for (int s = 128; s > 0; s >>= 1) {
-    if (tid < s) part[tid] += part[tid + s];
-    __syncthreads();
-  }
-  all = part[0];
+  before = place_block_sum(before, s_w);
+  all = place_block_sum(all, s_w);
   if (e == experts) {  // the tiles no pair fills: no expert, token 0
-    for (int t = all + tid; t < most; t += 256) {
+    for (int t = all + tid; t < most; t += PLACE_NT) {
       tile_expert[t] = experts;
       for (int j = 0; j < TOKENS_TILE; ++j) token[t * TOKENS_TILE + j] = 0;
     }
     return;
   }
   const int count = counts[e], tiles = (count + TOKENS_TILE - 1) / TOKENS_TILE;
-  for (int t = tid; t < tiles; t += 256) tile_expert[before + t] = e;
-  for (int j = count + tid; j < tiles * TOKENS_TILE; j += 256) token[before * TOKENS_TILE + j] = 0;
-  // the expert's pairs in order: a running count over the pairs, 256 at a time
+  for (int t = tid; t < tiles; t += PLACE_NT) tile_expert[before + t] = e;
+  for (int j = count + tid; j < tiles * TOKENS_TILE; j += PLACE_NT) token[before * TOKENS_TILE + j] = 0;
+  constexpr int RUN = 64 * PLACE_PER, BATCH = RUN * (PLACE_NT / 64);
   int seen = 0;
-  for (int base = 0; base < pairs; base += 256) {
-    int p = base + tid;
-    bool mine = p < pairs && flat[p] == e;
-    uint64_t ballot = __ballot(mine);
-    int rank_in_wave = __popcll(ballot & ((1ull << lane) - 1ull));
-    if (lane == 0) wave_n[wv] = __popcll(ballot);
-    __syncthreads();
-    int offset = seen;
-    for (int w = 0; w < wv; ++w) offset += wave_n[w];
-    if (mine) {
-      int slot = before * TOKENS_TILE + offset + rank_in_wave;
-      token[slot] = p / k;
-      where[p] = slot;
+  for (int b0 = 0; b0 < pairs; b0 += BATCH) {
+    const int p0 = b0 + wv * RUN + lane;  // the lane's pair of slot i: p0 + 64 i
+    int v[PLACE_PER];
+#pragma unroll
+    for (int i = 0; i < PLACE_PER; ++i) v[i] = p0 + 64 * i < pairs ? flat[p0 + 64 * i] : -1;
+    uint32_t bits = 0;
+    int n = 0;
+#pragma unroll
+    for (int i = 0; i < PLACE_PER; ++i) {
+      const bool mine = v[i] == e;
+      bits |= (uint32_t)mine << i;
+      n += __popcll(__ballot(mine));
     }
-    seen += wave_n[0] + wave_n[1] + wave_n[2] + wave_n[3];
+    if (lane == 0) s_w[wv] = n;
     __syncthreads();
+    int off = seen, total = 0;
+#pragma unroll
+    for (int w = 0; w < PLACE_NT / 64; ++w) {
+      const int c = s_w[w];
+      off += w < wv ? c : 0;
+      total += c;
+    }
+    __syncthreads();  // s_w is read by all before the next batch writes it
+    int run = before * TOKENS_TILE + off;
+#pragma unroll
+    for (int i = 0; i < PLACE_PER; ++i) {
+      const bool mine = (bits >> i) & 1u;
+      const uint64_t m = __ballot(mine);
+      if (mine) {
+        const int p = p0 + 64 * i, slot = run + __popcll(m & below);
+        token[slot] = p / k;
+        where[p] = slot;
+      }
+      run += __popcll(m);
+    }
+    seen += total;
   }
 }
 
@@ -287,7 +316,7 @@ int sh_tiles_of(const int32_t* flat, int64_t pairs, int64_t k, int64_t experts, 
                      (int)experts, counts);
   int st = check_launch("tiles_of");
   if (st) return st;
-  hipLaunchKernelGGL(k_tile_place, dim3((unsigned)experts + 1), dim3(256), 0, (hipStream_t)stream, flat, (int)pairs,
+  hipLaunchKernelGGL(k_tile_place, dim3((unsigned)experts + 1), dim3(PLACE_NT), 0, (hipStream_t)stream, flat, (int)pairs,
                      (int)k, (int)experts, counts, (int)most, tile_expert, token, where);
   return check_launch("tiles_of");
 }
