@@ -360,12 +360,13 @@ def tiles_of(indices: torch.Tensor, experts: int) -> tuple:
 
 
 def tile_matmul(blocks: torch.Tensor, kind: str, shape: tuple, a: torch.Tensor, tile_expert: torch.Tensor) -> torch.Tensor:
-    """out[p] = W[expert of p's tile] . a[p] for a stack of `shape` (experts, rows, cols); a (P, cols) float16 or
-    bfloat16, P a multiple of TOKENS_TILE; the weights rounded to a's type, float32 sums. Rows of a tile naming no
-    expert are left as they were (strata_mlx/blocks.py:516-536). Returns (P, rows) float32. The reference also
-    takes float32 activations; here they raise ValueError (switch_glu sends float32 prompts to the matvec)."""
-    if a.dtype not in (torch.float16, torch.bfloat16):
-        raise ValueError(f"tile_matmul: activations of {a.dtype} (float16 or bfloat16)")
+    """out[p] = W[expert of p's tile] . a[p] for a stack of `shape` (experts, rows, cols); a (P, cols) float16,
+    bfloat16 or float32, P a multiple of TOKENS_TILE; the weights rounded to a's type, float32 sums. Rows of a
+    tile naming no expert are left as they were (strata_mlx/blocks.py:516-536). Returns (P, rows) float32.
+    float32 activations take the weights exactly: each slot is then the expert matvec of its tile's expert
+    (switch_matvec's kernels), tiles naming no expert computed against expert 0 (their rows are unspecified)."""
+    if a.dtype not in (torch.float16, torch.bfloat16, torch.float32):
+        raise ValueError(f"tile_matmul: activations of {a.dtype} (float16, bfloat16 or float32)")
     experts, rows, cols = shape
     if not tileable(kind, rows, cols):
         raise ValueError(f"tile_matmul: {kind} ({rows}, {cols}) is not tileable")
@@ -376,6 +377,11 @@ def tile_matmul(blocks: torch.Tensor, kind: str, shape: tuple, a: torch.Tensor, 
     te = tile_expert.to(torch.int32).contiguous()
     if te.numel() * TOKENS_TILE != p:
         raise ValueError(f"tile_matmul: {te.numel()} tiles for {p} rows")
+    if a.dtype == torch.float32:
+        slot_expert = te.repeat_interleave(TOKENS_TILE)
+        slot_expert = torch.where((slot_expert >= 0) & (slot_expert < experts), slot_expert,
+                                  torch.zeros_like(slot_expert))
+        return switch_matvec(blocks, kind, shape, slot_expert, a, 1)
     _on_gpu(blocks, a, te)
     out = torch.empty((p, rows), dtype=torch.float32, device=a.device)
     _lib.call("sh_tile_matmul", _kind(kind), _u8(blocks).data_ptr(), _tabs(kind, a.device), experts, rows, cols,
@@ -455,10 +461,9 @@ def _tiled_glu(x, indices, up, gate, down):
 
 def switch_glu(x: torch.Tensor, indices: torch.Tensor, up, gate, down) -> torch.Tensor:
     """down(silu(gate(x)) * up(x)) through each token's experts: x (..., in), indices (..., experts per token)
-    (strata_mlx/blocks.py:801-829). The branches: a prompt's many pairs through the tiles (float16 / bfloat16;
-    the reference also tiles float32, which here takes the matvec); otherwise gate and up by the expert matvec
-    (one row of x to each token's k pairs) and down taking silu(gate) * up itself."""
-    if (indices.numel() >= TILES_FROM and x.dtype in (torch.float16, torch.bfloat16)
+    (strata_mlx/blocks.py:801-829). The branches: a prompt's many pairs through the tiles; otherwise gate and up
+    by the expert matvec (one row of x to each token's k pairs) and down taking silu(gate) * up itself."""
+    if (indices.numel() >= TILES_FROM and x.dtype in (torch.float16, torch.bfloat16, torch.float32)
             and all(tileable(lin.kind, lin.output_dims, lin.input_dims) for lin in (up, gate, down))):
         return _tiled_glu(x, indices, up, gate, down)
     if indices.numel() >= LOOKUP_FROM and all(lookable(lin, x.dtype) for lin in (up, gate, down)):

@@ -148,3 +148,36 @@ def test_the_fused_gate_up_is_swiglu_of_the_tile_products(tables, dev):
     diff = (h[real].float() - want[real].float()).abs()
     assert diff.max().item() <= 2 ** -7 * want[real].float().abs().max().item()
     assert (diff == 0).float().mean().item() > 0.99
+
+
+@pytest.mark.parametrize("kind", ["IQ3_S", "Q2_0", "Q3_K"])
+def test_float32_activations_take_the_weights_exactly(kind, tables, dev):
+    """tile_matmul with float32 activations (the weights exact, float32 sums) against float64 products, tiles in
+    any order; tiles naming no expert are not compared."""
+    shape = (3, 64, 512)
+    raw, w, rng = stack(kind, *shape, 9, tables)
+    tiles = np.array([2, 0, 3, 0, 1], dtype=np.int32)  # 3: no expert
+    a = torch.from_numpy(rng.standard_normal((16 * len(tiles), shape[2])).astype(np.float32))
+    got = SB.tile_matmul(torch.from_numpy(raw).to(dev), kind, shape, a.to(dev), torch.from_numpy(tiles).to(dev))
+    assert got.dtype == torch.float32
+    want = OT.tile_matmul(w, a.numpy(), tiles, "float32")
+    real = ~np.isnan(want)
+    assert np.abs(got.cpu().numpy()[real] - want[real]).max() <= 1e-5 * np.abs(want[real]).max()
+
+
+def test_a_float32_prompt_through_the_tiles(tables, dev):
+    """switch_glu's prompt branch in float32 (the reference tiles float16 and float32 prompts) against the
+    composition pair by pair."""
+    kind, E, F, D, T, K = "IQ3_S", 16, 256, 256, 256, 8
+    rng = np.random.default_rng(10)
+    raws, ws = {}, {}
+    for n, (r, c) in (("g", (F, D)), ("u", (F, D)), ("d", (D, F))):
+        raws[n], ws[n], _ = stack(kind, E, r, c, 20 + len(raws), tables)
+    lin = {n: SB.BlockSwitchLinear(torch.from_numpy(raws[n]).to(dev), kind, (E,) + ws[n].shape[1:]) for n in raws}
+    idx = OR.top_k(rng.standard_normal((T, E)).astype(np.float32), K)
+    assert idx.size >= SB.TILES_FROM
+    x = torch.from_numpy(rng.standard_normal((T, D)).astype(np.float32))
+    got = SB.BlockSwitchGLU(lin["g"], lin["u"], lin["d"])(x.to(dev), torch.from_numpy(idx).to(dev))
+    assert got.shape == (T, K, D) and got.dtype == torch.float32
+    want, _ = prompt_want(ws["g"], ws["u"], ws["d"], x, idx, "float32")
+    assert np.abs(got.cpu().numpy().reshape(-1, D) - want).max() <= 1e-4 * np.abs(want).max()
