@@ -6,7 +6,7 @@ the MoE block's combine, the prompt tiles and paged decode attention. Every func
 file:line it follows (paths relative to the strata-mlx repository).
 
 Only `tests/`, `__graft_entry__.smoke()` and the `cpu_baseline` leg of `bench.py` may import it, and only
-as the checker or the reported CPU baseline — never as the thing measured or shipped. The product package
+to check results or as the reported CPU baseline — never as the thing measured or shipped. The product package
 (`strata_hip`) does not import it and fails loudly when its HIP library is missing.
 
 Parity status of each function is stated in its docstring; "parity unpinned" marks content that no
