@@ -184,10 +184,11 @@ def attention_decode(dev, steps, warmup):
 
 def prefill_layer(dev, steps, warmup):
     """C5: a 2048-token prompt chunk through one MoE layer's routed experts: top-10 of 512 under Zipf(1.1)
-    popularity, IQ3_S experts (gate / up 512 x 2048, down 2048 x 512), pairs in tiles of 16 by tiles_of, the three
-    grouped GEMMs on MFMA with the weights dequantized into LDS as bf16. Timed: tiles_of + the three products +
-    the SwiGLU between them, as one captured graph. MFMA use = 2 * pairs * (3 * 512 * 2048) flops / time against
-    the 2.5 PFLOP/s dense bf16 peak."""
+    popularity, IQ3_S experts (gate / up 512 x 2048, down 2048 x 512), pairs in tiles of 16 by tiles_of, the
+    three grouped GEMMs on MFMA with the weights dequantized into LDS as bf16 (gate and up with the SwiGLU in one
+    pass, down with the un-permutation in another). Timed: tiles_of + both passes, as one captured graph (the
+    layer's whole prompt path after routing). MFMA use = 2 * pairs * (3 * 512 * 2048) flops / time against the
+    2.5 PFLOP/s dense bf16 peak."""
     import numpy as np
     import torch
 
