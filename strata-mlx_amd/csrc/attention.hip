@@ -261,55 +261,122 @@ __global__ __launch_bounds__(ATT_NT, 3) void k_attn_split(AttnArgs a) {  // (3 b
   }
 }
 
-// merge the splits of 16 rows x 16 dims (block (dim tile, row tile, unit x row group)):
+// merge the splits of 4 rows x 16 dims (block (dim tile, row quad, unit x row group)):
 // out = sum_s O_s 2^(m_s - m) / sum_s l_s 2^(m_s - m); a row that sees no position (every cell masked) gives zeros.
-// The 16 rows' factors of every split go to LDS first (16 threads a row); then thread t sums element t of the
-// tile's lane layout over the splits (256 consecutive floats a split: one coalesced read).
+// Its time is memory latency and the misses one CU keeps in flight, so the merge spreads over many small blocks
+// (a row quad's 64 floats of a dim tile: 256 consecutive bytes a split, a coalesced read a wave) and each thread keeps
+// many loads in flight. The block's 16 waves share the splits: wave w sums its sixteenth, in split order, and the
+// 16 sums add in wave order. Its first chunk of partial outputs is on the way while the block turns the 4 rows'
+// maxima and sums of every split (4 a thread, in one round) into factors in LDS. C, the loads of a chunk, is 8 when
+// that holds a sixteenth of the splits, else 16 (two chunks in flight).
 constexpr int ATT_MAX_SPLITS = 1024;
+constexpr int ATT_MERGE_NT = 1024;
 
-template <typename XT, int D, bool CELLS>
-__global__ __launch_bounds__(256) void k_attn_merge(AttnArgs a) {
-  extern __shared__ float fac[];  // [splits][16]
-  __shared__ float s_inv[16];
+template <typename XT, int D, bool CELLS, int C>
+__global__ __launch_bounds__(ATT_MERGE_NT) void k_attn_merge(AttnArgs a) {
+  extern __shared__ float fac[];  // [splits][4] maxima, then factors; then [splits][4] sums
+  __shared__ float s_red[2][16], s_inv[4];
+  __shared__ float s_part[16][64];
+  static_assert(ATT_MAX_SPLITS <= 4 * 256, "one round of 4 loads a thread covers the splits");
   constexpr int NDT = D / 16;
   const int tid = threadIdx.x;
   const int zgroups = CELLS ? 1 : (a.rows + 63) / 64;
-  const int dt = blockIdx.x, rt = blockIdx.y, unit = blockIdx.z / zgroups, zg = blockIdx.z % zgroups;
-  const int row0 = zg * 64 + rt * 16;
-  {
-    const int r = tid >> 4, j = tid & 15, row = row0 + r;
-    const bool real = row < a.rows;
-    const int64_t stride = (int64_t)a.units * a.rows;
-    const float* m0 = a.wm + (int64_t)unit * a.rows + row;
-    const float* l0 = a.wl + (int64_t)unit * a.rows + row;
-    float m = -INFINITY;
-    if (real)
-      for (int s2 = j; s2 < a.splits; s2 += 16) m = fmaxf(m, m0[s2 * stride]);
+  const int dt = blockIdx.x, quad = blockIdx.y, unit = blockIdx.z / zgroups, zg = blockIdx.z % zgroups;
+  const int row0 = zg * 64 + 4 * quad;
+  if (row0 >= a.rows) return;  // the last row group's padding quads (the whole block)
+  const int S = a.splits;
+  float* sums = fac + S * 4;
+  // wave w, lane t: element t of the quad's 64 floats (row row0 + t % 4, dim 16 dt + t / 4), splits [w Q, w Q + Q)
+  const int w = tid >> 6, t = tid & 63, Q = (S + 15) / 16, s_lo = w * Q;
+  const int64_t ostride = (int64_t)a.units * zgroups * 4 * NDT * 256;  // floats a split
+  const float* od = a.wo + ((((int64_t)unit * zgroups + zg) * 4 + (quad >> 2)) * NDT + dt) * 256 + 64 * (quad & 3) + t;
+  float v[C], w2[C];
 #pragma unroll
-    for (int o = 1; o < 16; o <<= 1) m = fmaxf(m, __shfl_xor(m, o));
-    const float base = m == -INFINITY ? 0.0f : m;
-    float l = 0.0f;
-    for (int s2 = j; s2 < a.splits; s2 += 16) {
-      const float f = real ? exp2f(m0[s2 * stride] - base) : 0.0f;
-      fac[s2 * 16 + r] = f;
-      if (real) l += l0[s2 * stride] * f;
+  for (int c = 0; c < C; ++c) v[c] = od[(int64_t)min(s_lo + c, S - 1) * ostride];
+  {
+    const int r = tid >> 8, j = tid & 255, row = row0 + r;  // 4 waves a row
+    const bool real = row < a.rows;
+    float m = -INFINITY;
+    if (real) {
+      const int64_t stride = (int64_t)a.units * a.rows;
+      const float* m0 = a.wm + (int64_t)unit * a.rows + row;
+      const float* l0 = a.wl + (int64_t)unit * a.rows + row;
+      float mv[4], lv[4];
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const int s2 = min(256 * c + j, S - 1);
+        mv[c] = m0[s2 * stride];
+        lv[c] = l0[s2 * stride];
+      }
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const int s2 = 256 * c + j;
+        if (s2 < S) {
+          fac[s2 * 4 + r] = mv[c];
+          sums[s2 * 4 + r] = lv[c];
+          m = fmaxf(m, mv[c]);
+        }
+      }
     }
 #pragma unroll
-    for (int o = 1; o < 16; o <<= 1) l += __shfl_xor(l, o);
-    if (j == 0) s_inv[r] = l > 0.0f ? 1.0f / l : 0.0f;
+    for (int o = 1; o < 64; o <<= 1) m = fmaxf(m, __shfl_xor(m, o));
+    if ((tid & 63) == 0) s_red[0][w] = m;
+    __syncthreads();
+    m = fmaxf(fmaxf(s_red[0][4 * r], s_red[0][4 * r + 1]), fmaxf(s_red[0][4 * r + 2], s_red[0][4 * r + 3]));
+    const float base = m == -INFINITY ? 0.0f : m;
+    float l = 0.0f;
+    for (int s2 = j; s2 < S; s2 += 256) {
+      float f = 0.0f;
+      if (real) {
+        f = exp2f(fac[s2 * 4 + r] - base);
+        l += sums[s2 * 4 + r] * f;
+      }
+      fac[s2 * 4 + r] = f;
+    }
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) l += __shfl_xor(l, o);
+    if ((tid & 63) == 0) s_red[1][w] = l;
   }
   __syncthreads();
-  const int ln = tid >> 2, i = tid & 3, rr = 4 * (ln >> 4) + i, row = row0 + rr, dim = 16 * dt + (ln & 15);
-  const int64_t ostride = (int64_t)a.units * zgroups * 4 * NDT * 256;  // floats a split
-  const float* od = a.wo + ((((int64_t)unit * zgroups + zg) * 4 + rt) * NDT + dt) * 256 + tid;
+  if (tid < 4) {
+    const float l = ((s_red[1][4 * tid] + s_red[1][4 * tid + 1]) + s_red[1][4 * tid + 2]) + s_red[1][4 * tid + 3];
+    s_inv[tid] = l > 0.0f ? 1.0f / l : 0.0f;
+  }
+  const int rq = t & 3, s_hi = min(s_lo + Q, S), nch = (Q + C - 1) / C;
   float acc = 0.0f;
-#pragma unroll 8
-  for (int s2 = 0; s2 < a.splits; ++s2) acc += od[s2 * ostride] * fac[s2 * 16 + rr];
-  if (row < a.rows) {
+  for (int k = 0; k < nch; k += 2) {
+    if (k + 1 < nch) {
+#pragma unroll
+      for (int c = 0; c < C; ++c) w2[c] = od[(int64_t)min(s_lo + (k + 1) * C + c, S - 1) * ostride];
+    }
+#pragma unroll
+    for (int c = 0; c < C; ++c) {
+      const int s2 = s_lo + k * C + c;
+      const float sum = acc + v[c] * fac[min(s2, S - 1) * 4 + rq];
+      acc = s2 < s_hi ? sum : acc;
+    }
+    if (k + 1 >= nch) break;
+    if (k + 2 < nch) {
+#pragma unroll
+      for (int c = 0; c < C; ++c) v[c] = od[(int64_t)min(s_lo + (k + 2) * C + c, S - 1) * ostride];
+    }
+#pragma unroll
+    for (int c = 0; c < C; ++c) {
+      const int s2 = s_lo + (k + 1) * C + c;
+      const float sum = acc + w2[c] * fac[min(s2, S - 1) * 4 + rq];
+      acc = s2 < s_hi ? sum : acc;
+    }
+  }
+  s_part[w][t] = acc;
+  __syncthreads();
+  const int row = row0 + rq;
+  if (w == 0 && row < a.rows) {
+#pragma unroll
+    for (int u = 1; u < 16; ++u) acc += s_part[u][t];
     const int group = a.hq / a.hkv;
     const int h = CELLS ? unit % a.hkv : unit;
     const int qt = CELLS ? unit / a.hkv : row / group, qh = h * group + (CELLS ? row : row % group);
-    ((XT*)a.out)[((int64_t)qt * a.hq + qh) * D + dim] = from_f32<XT>(acc * s_inv[rr]);
+    ((XT*)a.out)[((int64_t)qt * a.hq + qh) * D + 16 * dt + (t >> 2)] = from_f32<XT>(acc * s_inv[rq]);
   }
 }
 
@@ -380,9 +447,13 @@ template <typename XT, int D, bool CELLS> static int launch_attn(AttnArgs a, hip
   hipLaunchKernelGGL((k_attn_split<XT, D, CELLS>), dim3(a.splits, a.units, zgroups), dim3(ATT_NT), lds, stream, a);
   int st = check_launch("attention split");
   if (st) return st;
-  const int rtiles = (std::min(64, a.rows) + 15) / 16;  // row tiles of a row group (the last may hold fewer rows)
-  hipLaunchKernelGGL((k_attn_merge<XT, D, CELLS>), dim3(D / 16, rtiles, a.units * zgroups), dim3(256),
-                     (size_t)a.splits * 16 * sizeof(float), stream, a);
+  const int quads = (std::min(64, a.rows) + 3) / 4;  // row quads of a row group (the last group may hold fewer)
+  const dim3 mgrid(D / 16, quads, a.units * zgroups);
+  const size_t mlds = (size_t)a.splits * 2 * 4 * sizeof(float);
+  if ((a.splits + 15) / 16 <= 8)
+    hipLaunchKernelGGL((k_attn_merge<XT, D, CELLS, 8>), mgrid, dim3(ATT_MERGE_NT), mlds, stream, a);
+  else
+    hipLaunchKernelGGL((k_attn_merge<XT, D, CELLS, 16>), mgrid, dim3(ATT_MERGE_NT), mlds, stream, a);
   return check_launch("attention merge");
 }
 
