@@ -230,19 +230,32 @@ __global__ __launch_bounds__(ATT_NT, 3) void k_attn_split(AttnArgs a) {  // (3 b
       float l_all = 0.0f;
       for (int p2 = 0; p2 < PL; ++p2)
         l_all += red[ATT_WAVES * 64 + (p2 * RT4 + rt) * 64 + lane] * exp2f(red[(p2 * RT4 + rt) * 64 + lane] - base);
-      float fr[ATT_WAVES][4];
-      for (int p2 = 0; p2 < PL; ++p2)
+      // O rows 4g + i: phase by phase (the first is this wave's own), all NDT reads of a phase in flight at once
+      float bq[4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) fr[p2][i] = exp2f(red[(p2 * RT4 + rt) * 64 + 4 * g + i] - __shfl(base, 4 * g + i));
+      for (int i = 0; i < 4; ++i) bq[i] = __shfl(base, 4 * g + i);
+      for (int p2 = 0; p2 < PL; ++p2) {
+        float fr[4];
 #pragma unroll
-      for (int dt = 0; dt < NDT; ++dt) {
-        f32x4 o = {0.0f, 0.0f, 0.0f, 0.0f};
-        for (int p2 = 0; p2 < PL; ++p2) {
-          const f32x4 v = redo[((p2 * RT4 + rt) * NDT + dt) * 64 + lane];
+        for (int i = 0; i < 4; ++i) fr[i] = exp2f(red[(p2 * RT4 + rt) * 64 + 4 * g + i] - bq[i]);
+        if (p2 == 0) {
 #pragma unroll
-          for (int i = 0; i < 4; ++i) o[i] += v[i] * fr[p2][i];
+          for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              float o = 0.0f;
+              o += O[dt][i] * fr[i];
+              O[dt][i] = o;
+            }
+        } else {
+          f32x4 v[NDT];
+#pragma unroll
+          for (int dt = 0; dt < NDT; ++dt) v[dt] = redo[((p2 * RT4 + rt) * NDT + dt) * 64 + lane];
+#pragma unroll
+          for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) O[dt][i] += v[dt][i] * fr[i];
         }
-        O[dt] = o;
       }
       m_run = m_all;
       l_run = l_all;
