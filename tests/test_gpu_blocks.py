@@ -187,6 +187,24 @@ def test_stack_matvec_streams_many_matrices(kind, dtype, tokens, tables, dev):
     assert rel_err(got, want) <= TOL[dtype]
 
 
+@pytest.mark.parametrize("dtype", ["bfloat16", "float16"])
+@pytest.mark.parametrize("tokens", [1, 2])
+@pytest.mark.parametrize("shape", [(40, 512, 1024), (12, 1536, 2048)])
+def test_long_q2_stacks_stream_by_waves(shape, tokens, dtype, tables, dev):
+    """Q2_0 stacks of more than a thousand 16-row groups (the wave-streamed form): blocks whose row groups cross
+    matrix boundaries, waves with no row group in a block, 2 and 4 K-chunks a row."""
+    n, R, C = shape
+    raw, w = stack("Q2_0", n, R, C, 40 + tokens, tables)
+    rng = np.random.default_rng(50 + tokens)
+    x, xv = act(rng, (n, tokens, C), dtype)
+    got = SB.stack_matvec(torch.from_numpy(raw).to(dev), "Q2_0", (n, R, C), x.to(dev)).float().cpu().numpy()
+    want = np.stack([xv[m].astype(np.float64) @ w[m].T.astype(np.float64) for m in range(n)])
+    assert got.shape == (n, tokens, R)
+    assert rel_err(got, want) <= TOL[dtype]
+    for m in (0, n // 2, n - 1):  # every matrix's own rows
+        assert rel_err(got[m], want[m]) <= TOL[dtype]
+
+
 @pytest.mark.parametrize("kind", ["Q2_0", "IQ3_S"])
 def test_window_matvec_bits_do_not_depend_on_the_window(kind, tables, dev):
     raw, w = stack(kind, 1, 96, 2048, 30, tables)
