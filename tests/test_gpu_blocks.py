@@ -189,15 +189,16 @@ def test_stack_matvec_streams_many_matrices(kind, dtype, tokens, tables, dev):
 
 @pytest.mark.parametrize("dtype", ["bfloat16", "float16"])
 @pytest.mark.parametrize("tokens", [1, 2])
-@pytest.mark.parametrize("shape", [(40, 512, 1024), (12, 1536, 2048)])
-def test_long_q2_stacks_stream_by_waves(shape, tokens, dtype, tables, dev):
-    """Q2_0 stacks of more than a thousand 16-row groups (the wave-streamed form): blocks whose row groups cross
-    matrix boundaries, waves with no row group in a block, 2 and 4 K-chunks a row."""
+@pytest.mark.parametrize("kind, shape", [("Q2_0", (40, 512, 1024)), ("Q2_0", (12, 1536, 2048)),
+                                         ("IQ3_S", (40, 512, 2048)), ("IQ3_S", (12, 1536, 2048))])
+def test_long_stacks_stream_by_waves(kind, shape, tokens, dtype, tables, dev):
+    """Stacks of more than a thousand 16-row groups: Q2_0 in the wave-streamed form (blocks whose row groups cross
+    matrix boundaries, waves with no row group in a block, 2 and 4 K-chunks a row), IQ3_S in the block-ring form."""
     n, R, C = shape
-    raw, w = stack("Q2_0", n, R, C, 40 + tokens, tables)
+    raw, w = stack(kind, n, R, C, 40 + tokens, tables)
     rng = np.random.default_rng(50 + tokens)
     x, xv = act(rng, (n, tokens, C), dtype)
-    got = SB.stack_matvec(torch.from_numpy(raw).to(dev), "Q2_0", (n, R, C), x.to(dev)).float().cpu().numpy()
+    got = SB.stack_matvec(torch.from_numpy(raw).to(dev), kind, (n, R, C), x.to(dev)).float().cpu().numpy()
     want = np.stack([xv[m].astype(np.float64) @ w[m].T.astype(np.float64) for m in range(n)])
     assert got.shape == (n, tokens, R)
     assert rel_err(got, want) <= TOL[dtype]
