@@ -193,31 +193,34 @@ __global__ __launch_bounds__(NWMAX * 64) void k_stack_mv(const uint8_t* __restri
 
 // ---- Q2_0 stacks for 1 to 4 tokens (taken for 1 and 2), streamed by independent waves (rows a multiple of 16,
 // columns of 512).
-// A block's waves share nothing per item: each wave streams its own tasks (16 rows x 8 blocks: 512 columns of a
-// row group, 2,304 bytes) through its own LDS ring of direct loads and waits only on its own loads, so a wave's
-// multiply overlaps the other waves' memory time with no barrier between them. The block's row groups (a
-// contiguous range of the stack) are taken in units of one matrix: at a unit's start the block meets, turns the
-// matrix's activations into the MFMA fragments (each value scaled by the unit of the mask that decodes its code)
-// and the offset sums in LDS, and meets again; within a unit wave w takes row groups w, w + 4, ..., all K-chunks
-// of one before the next. Outputs wait in LDS and are stored when the block is done.
+// A block's waves share nothing per item: each wave streams its own tasks (a row tile of 32 rows, or 16 when the
+// matrix's rows are not a multiple of 32, x 8 blocks: 512 columns, 144 bytes a row) through its own LDS ring of
+// direct loads and waits only on its own loads, so a wave's multiply overlaps the other waves' memory time with
+// no barrier between them; each activation fragment read from LDS serves the tile's row groups. The block's row
+// tiles (a contiguous range of the stack) are taken in units of one matrix: at a unit's start the block meets,
+// turns the matrix's activations into the MFMA fragments (each value scaled by the unit of the mask that decodes
+// its code) and the offset sums in LDS, and meets again; within a unit wave w takes row tiles w, w + 4, ..., all
+// K-chunks of one before the next. Outputs wait in LDS and are stored when the block is done.
 constexpr int SQ_WAVES = 4, SQ_KC = 8;  // waves a block; Q2_0 blocks (64 columns each) a K-chunk
-constexpr int SQ_SLOT = 16 * SQ_KC * 18;  // a task's bytes: 16 rows x 144
-constexpr int SQ_NI = 3;                  // direct loads a task: 144 16-byte chunks as 64 + 64 + 16
-constexpr int SQ_NS = 4;                  // ring slots a wave: three tasks in flight while one is multiplied
+// a task: RT row groups (16 RT rows) x SQ_KC blocks, 144 bytes a row, read as 9 RT 16-byte chunks a row group
+template <int RT> constexpr int sq_slot() { return RT * 16 * 144; }
+template <int RT> constexpr int sq_ni() { return (RT * 144 + 63) / 64; }  // direct loads a task
+template <int RT> constexpr int sq_ns() { return RT == 1 ? 4 : 3; }      // ring slots a wave
 
 struct SqPlan {
   int rows, cols, tokens, ng, nkc;  // ng: 64-column groups a row; nkc: K-chunks a row
   int64_t rbytes, mat_bytes;
-  int rgm;         // row groups a matrix
-  int total, rg0;  // row groups of the stack (< 2^31); the launch's first
-  int per;         // row groups a block
+  int rgm;         // row tiles (16 RT rows) a matrix
+  int total, rg0;  // row tiles of the stack (< 2^31); the launch's first
+  int per;         // row tiles a block
   int xs_off, nc_off, pt_off, out_off, ring_off;  // LDS byte offsets
 };
 
-template <typename XT>
+template <typename XT, int RT>
 __global__ __launch_bounds__(SQ_WAVES * 64) void k_stack_q2(const uint8_t* __restrict__ blocks, SqPlan P,
                                                             const XT* __restrict__ x, XT* __restrict__ out) {
   using MT = XT;
+  constexpr int SQ_SLOT = sq_slot<RT>(), SQ_NI = sq_ni<RT>(), SQ_NS = sq_ns<RT>(), TR = 16 * RT;
   extern __shared__ u32x4 dyn[];
   uint8_t* lds = (uint8_t*)dyn;
   const uint32_t lds_base = SH_LDS_ADDR(dyn);
@@ -229,7 +232,7 @@ __global__ __launch_bounds__(SQ_WAVES * 64) void k_stack_q2(const uint8_t* __res
   const int xst = P.ng * 8 + 1;           // (a token's fragments one 16-byte entry more: distinct banks)
   float* ncs = (float*)(lds + P.nc_off);  // [group][token]: minus the offsets' sum
   float* pt = (float*)(lds + P.pt_off);   // [token][group][lane group]: the sum's four parts
-  XT* obuf = (XT*)(lds + P.out_off);      // [row group - A][token][16 rows]
+  XT* obuf = (XT*)(lds + P.out_off);      // [row tile - A][token][16 RT rows]
   const uint32_t ring = lds_base + P.ring_off + wave * SQ_NS * SQ_SLOT;
   const uint8_t* ringp = lds + P.ring_off + wave * SQ_NS * SQ_SLOT;
 
@@ -238,7 +241,7 @@ __global__ __launch_bounds__(SQ_WAVES * 64) void k_stack_q2(const uint8_t* __res
   uint32_t coff[SQ_NI];
 #pragma unroll
   for (int i = 0; i < SQ_NI; ++i) {
-    const int c = min(64 * i + lane, 16 * 9 - 1);
+    const int c = min(64 * i + lane, TR * 9 - 1);
     coff[i] = (uint32_t)((c / 9) * P.rbytes + 16 * (c % 9));
   }
   // a wave's tasks: (row group, K-chunk), units in order, row groups w, w + 4, ... of each, K-chunks in order
@@ -263,12 +266,12 @@ __global__ __launch_bounds__(SQ_WAVES * 64) void k_stack_q2(const uint8_t* __res
     if (c.rg >= c.ue) settle(c, c.ue, c.m + 1);
   };
   auto issue = [&](const Cur& c, int slot) {
-    const int r0 = (c.rg - c.m * P.rgm) * 16;
+    const int r0 = (c.rg - c.m * P.rgm) * TR;
     const uint8_t* src = blocks + (int64_t)c.m * P.mat_bytes + (int64_t)r0 * P.rbytes + c.kc * (SQ_KC * 18);
     const uint32_t dst = ring + slot * SQ_SLOT;
-    lds_dma16(src, coff[0], dst);
-    lds_dma16(src, coff[1], dst + 1024);
-    if (lane < 16) lds_dma16(src, coff[2], dst + 2048);
+#pragma unroll
+    for (int i = 0; i < SQ_NI - 1; ++i) lds_dma16(src, coff[i], dst + 1024 * i);
+    if (lane < TR * 9 - 64 * (SQ_NI - 1)) lds_dma16(src, coff[SQ_NI - 1], dst + 1024 * (SQ_NI - 1));
   };
 
   Cur ci, cc;
@@ -283,7 +286,9 @@ __global__ __launch_bounds__(SQ_WAVES * 64) void k_stack_q2(const uint8_t* __res
   const DecodeRegs kr = decode_regs<Q2_0, MT>();
   const int tok_n = (n & 3) == 0 && (n >> 2) < P.tokens ? n >> 2 : 0;  // the lane's A-row token (TPG 1 layout)
   const int tok_g = min(g, P.tokens - 1);                             // its D-row 4g's token
-  float acc = 0.0f;
+  float acc[RT];
+#pragma unroll
+  for (int r = 0; r < RT; ++r) acc[r] = 0.0f;
   for (int us = A, m = m_first; us < Bend; ++m) {
     const int ue = min(Bend, (m + 1) * P.rgm);
     __syncthreads();  // every wave is done with the last unit's fragments
@@ -329,22 +334,27 @@ __global__ __launch_bounds__(SQ_WAVES * 64) void k_stack_q2(const uint8_t* __res
         wait_vmcnt(SQ_NI * (n_issued - 1 - n_done));
       const uint8_t* slot = ringp + (n_done % SQ_NS) * SQ_SLOT + n * (SQ_KC * 18);
       const int gb = cc.kc * SQ_KC;
-      uint32_t w0[SQ_KC], w1[SQ_KC], dh[SQ_KC];
+      uint32_t w0[RT][SQ_KC], w1[RT][SQ_KC], dh[RT][SQ_KC];
       u32x4 xa[SQ_KC], xb[SQ_KC];
       float nc[SQ_KC];
 #pragma unroll
       for (int j = 0; j < SQ_KC; ++j) {
-        const uint8_t* b = slot + j * 18;
-        w0[j] = *(const uint16_t*)(b + 2 + 2 * g);
-        w1[j] = *(const uint16_t*)(b + 10 + 2 * g);
-        dh[j] = *(const uint16_t*)b;
+#pragma unroll
+        for (int r = 0; r < RT; ++r) {
+          const uint8_t* b = slot + r * 16 * (SQ_KC * 18) + j * 18;
+          w0[r][j] = *(const uint16_t*)(b + 2 + 2 * g);
+          w1[r][j] = *(const uint16_t*)(b + 10 + 2 * g);
+          dh[r][j] = *(const uint16_t*)b;
+        }
         xa[j] = xs[tok_n * xst + ((gb + j) * 2 + 0) * 4 + g];
         xb[j] = xs[tok_n * xst + ((gb + j) * 2 + 1) * 4 + g];
         nc[j] = ncs[(gb + j) * P.tokens + tok_g];
       }
 #pragma unroll
-      for (int j = 0; j < SQ_KC; ++j) {
-        const uint32_t W = w0[j] | (w1[j] << 16), W8 = W >> 8;
+      for (int j = 0; j < SQ_KC; ++j)
+#pragma unroll
+      for (int r = 0; r < RT; ++r) {
+        const uint32_t W = w0[r][j] | (w1[r][j] << 16), W8 = W >> 8;
         u32x4 fa, fb;
         fa.x = (W & kr.m0) | kr.magic;
         fa.y = (W & kr.m1) | kr.magic;
@@ -361,11 +371,14 @@ __global__ __launch_bounds__(SQ_WAVES * 64) void k_stack_q2(const uint8_t* __res
         }
         f32x4 D = mfma<MT>(xa[j], fa, f32x4{0.0f, 0.0f, 0.0f, 0.0f});
         D = mfma<MT>(xb[j], fb, D);
-        acc = fmaf(half_bits(dh[j]), D[0] + nc[j], acc);
+        acc[r] = fmaf(half_bits(dh[r][j]), D[0] + nc[j], acc[r]);
       }
-      if (cc.kc == P.nkc - 1) {  // the row group is done: lane (g, n) holds token g's row n
-        if (g < P.tokens) obuf[((cc.rg - A) * P.tokens + g) * 16 + n] = from_f32<XT>(acc);
-        acc = 0.0f;
+      if (cc.kc == P.nkc - 1) {  // the row tile is done: lane (g, n) holds token g's row 16 r + n
+#pragma unroll
+        for (int r = 0; r < RT; ++r) {
+          if (g < P.tokens) obuf[((cc.rg - A) * P.tokens + g) * TR + 16 * r + n] = from_f32<XT>(acc[r]);
+          acc[r] = 0.0f;
+        }
       }
       ++n_done;
     }
@@ -373,18 +386,20 @@ __global__ __launch_bounds__(SQ_WAVES * 64) void k_stack_q2(const uint8_t* __res
   }
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
-  const int nout = (Bend - A) * P.tokens * 16;
+  const int nout = (Bend - A) * P.tokens * TR;
   for (int e = tid; e < nout; e += SQ_WAVES * 64) {
-    const int rg = A + e / (P.tokens * 16);
-    const int t = (e / 16) % P.tokens;
-    const int m = rg / P.rgm, row = (rg - m * P.rgm) * 16 + (e & 15);
+    const int rg = A + e / (P.tokens * TR);
+    const int t = (e / TR) % P.tokens;
+    const int m = rg / P.rgm, row = (rg - m * P.rgm) * TR + e % TR;
     out[((int64_t)m * P.tokens + t) * P.rows + row] = obuf[e];
   }
 }
 
-template <typename XT>
+template <typename XT, int RT>
 static int launch_stack_q2(const uint8_t* blocks, int64_t n_mats, int64_t rows, int64_t cols, const XT* x,
                            int64_t tokens, XT* out, hipStream_t stream) {
+  constexpr int TR = 16 * RT;
+  constexpr size_t ring = (size_t)SQ_WAVES * sq_ns<RT>() * sq_slot<RT>();
   SqPlan P{};
   P.rows = (int)rows;
   P.cols = (int)cols;
@@ -393,11 +408,11 @@ static int launch_stack_q2(const uint8_t* blocks, int64_t n_mats, int64_t rows, 
   P.nkc = (int)(cols / (64 * SQ_KC));
   P.rbytes = row_bytes(Q2_0, cols);
   P.mat_bytes = rows * P.rbytes;
-  P.rgm = (int)(rows / 16);
+  P.rgm = (int)(rows / TR);
   P.total = (int)(n_mats * P.rgm);
   const size_t xs = (size_t)tokens * (P.ng * 8 + 1) * 16, nc = (size_t)P.ng * tokens * 4, pt = (size_t)tokens * P.ng * 16;
   const size_t out_cap = 16 * 1024;  // outputs a block holds at most
-  const int per_cap = (int)(out_cap / (tokens * 16 * sizeof(XT)));
+  const int per_cap = (int)(out_cap / (tokens * TR * sizeof(XT)));
   P.xs_off = 0;
   P.nc_off = (int)xs;
   P.pt_off = (int)(xs + nc);
@@ -408,21 +423,21 @@ static int launch_stack_q2(const uint8_t* blocks, int64_t n_mats, int64_t rows, 
   size_t lds = 0;
   for (; per_cu >= 1; --per_cu) {
     per = (int)std::min<int64_t>(per_cap, (P.total + (int64_t)cus * per_cu - 1) / ((int64_t)cus * per_cu));
-    const size_t ob = ((size_t)per * tokens * 16 * sizeof(XT) + 15) & ~(size_t)15;
-    lds = ((fixed + 15) & ~(size_t)15) + ob + (size_t)SQ_WAVES * SQ_NS * SQ_SLOT;
+    const size_t ob = ((size_t)per * tokens * TR * sizeof(XT) + 15) & ~(size_t)15;
+    lds = ((fixed + 15) & ~(size_t)15) + ob + ring;
     if ((size_t)per_cu * lds <= 160 * 1024) break;
   }
   if (per_cu < 1) return fail(E_UNSUPPORTED, "stack_matvec: %zu bytes of LDS", lds);
   P.per = per;
   P.out_off = (int)((fixed + 15) & ~(size_t)15);
-  P.ring_off = (int)(lds - (size_t)SQ_WAVES * SQ_NS * SQ_SLOT);
-  if ((size_t)P.ring_off + (size_t)SQ_WAVES * SQ_NS * SQ_SLOT > 128 * 1024)
+  P.ring_off = (int)(lds - ring);
+  if (lds > 128 * 1024)
     return fail(E_UNSUPPORTED, "stack_matvec: ring past the direct-load range");
   const int64_t grid = (int64_t)cus * per_cu, window = grid * per;
   for (int64_t r = 0; r < P.total; r += window) {
     P.rg0 = (int)r;
     const int64_t nb = std::min<int64_t>(grid, (P.total - r + per - 1) / per);
-    hipLaunchKernelGGL(k_stack_q2<XT>, dim3((unsigned)nb), dim3(SQ_WAVES * 64), lds, stream, blocks, P, x, out);
+    hipLaunchKernelGGL((k_stack_q2<XT, RT>), dim3((unsigned)nb), dim3(SQ_WAVES * 64), lds, stream, blocks, P, x, out);
     const int st = check_launch("stack_matvec");
     if (st) return st;
   }
@@ -534,9 +549,12 @@ int sh_stack_matvec(int kind, const void* blocks, const void* tables, int64_t n_
                          n_mats * (rows / 16) < (1ll << 31);
   return with_half_dtype(x_dtype, [&](auto* tp) {
     using XT = std::remove_pointer_t<decltype(tp)>;
+    if (q2_stream && rows % 32 == 0)
+      return launch_stack_q2<XT, 2>((const uint8_t*)blocks, n_mats, rows, cols, (const XT*)x, tokens, (XT*)out,
+                                    (hipStream_t)stream);
     if (q2_stream)
-      return launch_stack_q2<XT>((const uint8_t*)blocks, n_mats, rows, cols, (const XT*)x, tokens, (XT*)out,
-                                 (hipStream_t)stream);
+      return launch_stack_q2<XT, 1>((const uint8_t*)blocks, n_mats, rows, cols, (const XT*)x, tokens, (XT*)out,
+                                    (hipStream_t)stream);
     auto go = [&](auto kc, auto gc, auto tc) {
       constexpr int K = decltype(kc)::value, G = decltype(gc)::value, T = decltype(tc)::value;
       if (rw2)

@@ -190,10 +190,12 @@ def test_stack_matvec_streams_many_matrices(kind, dtype, tokens, tables, dev):
 @pytest.mark.parametrize("dtype", ["bfloat16", "float16"])
 @pytest.mark.parametrize("tokens", [1, 2])
 @pytest.mark.parametrize("kind, shape", [("Q2_0", (40, 512, 1024)), ("Q2_0", (12, 1536, 2048)),
-                                         ("IQ3_S", (40, 512, 2048)), ("IQ3_S", (12, 1536, 2048))])
+                                         ("Q2_0", (36, 528, 1024)), ("IQ3_S", (40, 512, 2048)),
+                                         ("IQ3_S", (12, 1536, 2048))])
 def test_long_stacks_stream_by_waves(kind, shape, tokens, dtype, tables, dev):
-    """Stacks of more than a thousand 16-row groups: Q2_0 in the wave-streamed form (blocks whose row groups cross
-    matrix boundaries, waves with no row group in a block, 2 and 4 K-chunks a row), IQ3_S in the block-ring form."""
+    """Stacks of more than a thousand 16-row groups: Q2_0 in the wave-streamed form (blocks whose row tiles cross
+    matrix boundaries, waves with no row tile in a block, 2 and 4 K-chunks a row, tiles of 32 rows and, for 528
+    rows a matrix, of 16), IQ3_S in the block-ring form."""
     n, R, C = shape
     raw, w = stack(kind, n, R, C, 40 + tokens, tables)
     rng = np.random.default_rng(50 + tokens)
