@@ -244,12 +244,12 @@ __global__ __launch_bounds__(SQ_WAVES * 64) void k_stack_q2(const uint8_t* __res
     const int c = min(64 * i + lane, TR * 9 - 1);
     coff[i] = (uint32_t)((c / 9) * P.rbytes + 16 * (c % 9));
   }
-  // a wave's tasks: (row group, K-chunk), units in order, row groups w, w + 4, ... of each, K-chunks in order
+  // a wave's tasks: (row tile, K-chunk), units in order, row tiles w, w + 4, ... of each, K-chunks in order
   struct Cur {
-    int rg, ue, m, kc;  // the row group (-1: no more), its unit's end and matrix, the K-chunk
+    int rg, ue, m, kc;  // the row tile (-1: no more), its unit's end and matrix, the K-chunk
   };
   const int m_first = A / P.rgm;
-  auto settle = [&](Cur& c, int us, int m) {  // the first unit from us (of matrix m) holding a row group of the wave
+  auto settle = [&](Cur& c, int us, int m) {  // the first unit from us (of matrix m) holding a row tile of the wave
     c.m = m;
     c.ue = min(Bend, (m + 1) * P.rgm);
     while (us < Bend && us + wave >= c.ue) {
