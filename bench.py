@@ -309,8 +309,8 @@ def main():
     ap.add_argument("--no-prefill", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1:
-        print(f"bench.py: --gpus {args.gpus}: this path is measured on one GPU (expert parallelism across GPUs is "
-              f"a design, not part of this build); run with --gpus 1", file=sys.stderr)
+        print(f"bench.py: --gpus {args.gpus}: this path runs and is measured on one GPU (expert parallelism across "
+              f"GPUs is not implemented); run with --gpus 1", file=sys.stderr)
         sys.exit(2)
 
     import numpy as np
