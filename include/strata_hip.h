@@ -145,6 +145,11 @@ int sh_moe_decode(int kind, int kind_down, const void* gate, const void* up, con
                   const void* tables, const void* logits, int logits_dtype, const void* x, int dtype, int64_t tokens,
                   int64_t k, int64_t d_model, int64_t d_ff, void* out, int32_t* idx_out, float* w_out,
                   void* workspace, size_t workspace_bytes, void* stream);
+/* No counterpart in the reference (a tuning knob for callers and tests): windows of at most `upto` tokens (0..16)
+ * have the routed outputs combined by the down kernel's last block of each row tile, larger ones by a combine kernel
+ * after it (default 4). Both give the same bits. Returns the previous bound. Process-wide; not for use while
+ * another thread launches sh_moe_decode. */
+int sh_moe_set_tail_combine(int upto);
 /* One of sh_moe_decode's kernels alone (phase 0 route, 1 gate/up, 2 down + combine; for the two-kernel shape
  * phases 0 and 1 are both the route + gate/up kernel), in that order over one workspace: what a caller times or
  * interleaves kernel by kernel. */

@@ -6,7 +6,8 @@ the generic branch 819-829: gate and up products rounded to the activation type,
 -> shared expert and its gate -> moe_combine (fused.py:448-481).
 
 Products are float64 over the exact float32 weights; every value the reference keeps in the activation type is
-rounded to it here. Tolerance against this: 1e-2 of max|want| for bfloat16 outputs.
+rounded to it here. Tolerance against this: 1e-2 of max|want| for bfloat16 outputs. The composition is pinned in
+tests/test_oracle_route.py on a two-expert block worked out by hand (top-1, and a top-2 tie ending in a bf16 tie).
 """
 
 import numpy as np

@@ -1,16 +1,17 @@
 """numpy restatement of the router's choice, SwiGLU and the MoE block's end (strata_mlx/fused.py, blocks.py).
 
 Parity:
-  * top_k — pinned: the order is a sort by (-value, index), i.e. `argpartition`'s stable order that
-    tests/test_fused.py:111-120 checks (fused.py:400-418, ties to the lower index at 411); tests check it
-    against brute force, ties included.
-  * routing_weights — pinned by closed form: softmax over the chosen float32 logits (fused.py:491), which
-    equals the full softmax renormalised over the chosen experts (checked in the tests).
+  * top_k — the order is a sort by (-value, index), i.e. `argpartition`'s stable order that
+    tests/test_fused.py:111-120 checks (fused.py:400-418, ties to the lower index at 411). Pinned in
+    tests/test_oracle_route.py against a brute-force sort, ties, equal rows and infinities included.
+  * routing_weights — softmax over the chosen float32 logits (fused.py:491). Pinned against the full softmax
+    renormalised over the chosen experts and closed forms (equal logits, e^ln3 : e^0).
   * swiglu — the rounding of blocks.py:222-237 (`_MATVEC_GLU`: sigmoid in float32 rounded to the
-    activations' type, then two products in that type); pinned against float64 silu(g)*u within the
-    rounding it documents.
-  * moe_combine — the order and roundings of fused.py:448-462 (`_COMBINE`), float32 scalar steps; pinned
-    against float64 sum_k y_k w_k + sigmoid(g) s within the documented roundings.
+    activations' type, then two products in that type). Pinned against float64 silu(g)*u within three
+    roundings and on closed cases (g = 0, sigma rounding to 1, sigma(1) in each type).
+  * moe_combine — the order and roundings of fused.py:448-462 (`_COMBINE`), float32 scalar steps. Pinned
+    against float64 sum_k y_k w_k + sigmoid(g) s within the documented roundings, and on hand-built cases
+    that a left fold, a fused multiply-add or a missing rounding of the routed sum would change.
 """
 
 import numpy as np
@@ -64,7 +65,8 @@ def routing_weights(logits: np.ndarray, idx: np.ndarray) -> np.ndarray:
 def sigmoid32(x: np.ndarray) -> np.ndarray:
     """float32 sigmoid in the form blocks.py:232-234 uses: y = 1/(1+exp(|g|)); g<0 ? y : 1-y."""
     x = np.asarray(x, dtype=f32)
-    y = (f32(1) / (f32(1) + np.exp(np.abs(x).astype(np.float64)).astype(f32))).astype(f32)
+    with np.errstate(over="ignore"):  # exp(|g|) past float32's range: 1 / inf = 0, as the kernel's float32 gives
+        y = (f32(1) / (f32(1) + np.exp(np.abs(x).astype(np.float64)).astype(f32))).astype(f32)
     return np.where(x < 0, y, (f32(1) - y)).astype(f32)
 
 

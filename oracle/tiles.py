@@ -2,7 +2,8 @@
 
 Parity:
   * tiles_of — strata_mlx/blocks.py:539-563, with a stable sort (pairs of one expert keep their order).
-    Pinned by the exact invariants of tests/test_blocks.py:177-195, checked in the tests.
+    Pinned by the exact invariants of tests/test_blocks.py:177-195 and the layout blocks.py:549-557 fixes,
+    checked in tests/test_oracle_route.py.
   * tile_matmul — blocks.py:465-536: out[p] = W[expert of p's tile] . a[p], the weights rounded to a's type,
     float32 sums; pinned against float64 products (tests/test_blocks.py:97-109, 2e-6 relative).
 """

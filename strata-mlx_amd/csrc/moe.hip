@@ -16,6 +16,8 @@
 // Only weights go through LDS: the activations each kernel multiplies were written by the kernel before in the
 // order its MFMA fragments take them, and are read straight from memory (L2). Grids are sized by the most groups
 // there could be (B*k + 1); blocks past the groups the route found leave at once, so nothing waits on the host.
+#include <atomic>
+
 #include "launch.h"
 #include "regmac.h"
 #include "xmv.h"
@@ -404,6 +406,8 @@ __global__ __launch_bounds__(256) void k_moe_gate_up(const uint8_t* __restrict__
 constexpr int FRONT_E = 512, FRONT_D = 2048, FRONT_F = 512;
 constexpr int FRONT_WAVES = 8;
 constexpr int TAIL_COMBINE_UPTO = 4;  // tokens up to which the tail combines in-kernel
+// the same bound as set at run time (sh_moe_set_tail_combine): 0 sends every window to the combine kernel
+static std::atomic<int> g_tail_combine_upto{TAIL_COMBINE_UPTO};
 
 // the pairs of group expert e in token order, into this wave's wp[0, n): pair t * K + j of each token t choosing e
 // (a token chooses an expert at most once), or every token's shared pair P + t for the shared expert (e == E)
@@ -860,19 +864,23 @@ __global__ __launch_bounds__(FRONT_WAVES * 64) void k_moe_tail(const uint8_t* __
   lds_sync();
   store_y();
   if (!combine) return;
-  // Count this block's items into their row tiles' counters once every output of them is out (vmcnt 0: the
-  // device-scope stores reached memory); the block that completes a tile's count combines the tile, reading the
-  // outputs with device-scope loads, and clears the counter. No device-wide fence: its L2 write-back and
-  // invalidation serialize the blocks of an XCD.
+  // Count this block's items into their row tiles' counters once every output of them is out; the block that
+  // completes a tile's count combines the tile and clears the counter. The hand-off is release / acquire at agent
+  // scope: the block's outputs are ordered before its counts by one release fence (after the barrier that joins
+  // every wave's stores), and a combining block's reads after its counts by one acquire fence. The outputs
+  // themselves are agent-scope stores and loads, so neither fence has much to write back or invalidate.
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
   if (tid < last - first) {
     const int tile = (first + tid) % TILES;
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
     if (__hip_atomic_fetch_add(&ws.cnt[tile], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == groups - 1)
       s_comb[atomicAdd(&s_ncomb, 1)] = tile;
   }
   __syncthreads();
   const int ncomb = s_ncomb;
+  if (ncomb == 0) return;
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
   for (int qv = tid; qv < ncomb * B * IT::ROWS; qv += NT) {
     const int c = qv / (B * IT::ROWS), rest = qv - c * (B * IT::ROWS);
     const int t = rest / IT::ROWS, row = s_comb[c] * IT::ROWS + rest % IT::ROWS;
@@ -1186,7 +1194,7 @@ static int launch_moe(const uint8_t* gate, const uint8_t* up, const uint8_t* dow
       return fail(E_UNSUPPORTED, "moe_decode: %lld blocks for the tail", (long long)grid);  // most TILES)
     // a few tokens: the tail's last block of a row tile combines it (no third launch); more: a combine kernel
     // (the tiles' last blocks would each combine several tiles, serially)
-    const int combine = B <= TAIL_COMBINE_UPTO;
+    const int combine = B <= g_tail_combine_upto.load(std::memory_order_relaxed);
     if constexpr (KIND_DOWN == Q2_0) {
       if (std::min<int64_t>(B * K, E) + 1 <= TAIL1_WAVES) {  // few groups: a block a 16-row tile, a wave a group
         constexpr int LOADS = (16 * (int)row_bytes_dev(Q2_0, FRONT_F) / 16 + 63) / 64;
@@ -1335,6 +1343,12 @@ int sh_moe_decode(int kind, int kind_down, const void* gate, const void* up, con
   return moe_decode(7, kind, kind_down, gate, up, down, experts, shared_gate, shared_up, shared_down, shared_gate_w,
                     tables, logits, logits_dtype, x, dtype, tokens, k, d_model, d_ff, out, idx_out, w_out, workspace,
                     workspace_bytes, stream);
+}
+
+int sh_moe_set_tail_combine(int upto) {
+  if (upto < 0 || upto > MOE_MAX_TOKENS)
+    return fail(E_ARG, "moe_set_tail_combine: %d tokens (0 to %d)", upto, MOE_MAX_TOKENS);
+  return g_tail_combine_upto.exchange(upto);
 }
 
 int sh_moe_decode_phase(int phase, int kind, int kind_down, const void* gate, const void* up, const void* down,

@@ -45,6 +45,7 @@ PROTOTYPES = {
     "sh_stack_matvec": [c_int, c_vp, c_vp, c_i64, c_i64, c_i64, c_vp, c_int, c_i64, c_vp, c_vp, c_sz, c_vp],
     "sh_moe_decode_phase": [c_int, c_int, c_int, c_vp, c_vp, c_vp, c_i64, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_int,
                             c_vp, c_int, c_i64, c_i64, c_i64, c_i64, c_vp, c_vp, c_sz, c_vp],
+    "sh_moe_set_tail_combine": [c_int],
     "sh_tile_matmul": [c_int, c_vp, c_vp, c_i64, c_i64, c_i64, c_vp, c_int, c_i64, c_vp, c_vp, c_vp],
     "sh_tile_glu": [c_int, c_vp, c_vp, c_vp, c_i64, c_i64, c_i64, c_vp, c_int, c_i64, c_vp, c_i64, c_vp, c_vp,
                     c_vp],

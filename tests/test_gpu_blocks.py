@@ -7,6 +7,7 @@ import torch
 
 from conftest import rel_err
 from oracle import blocks as OB
+from oracle import lookup as OL
 from oracle import route as OR
 from strata_hip import blocks as SB
 from strata_hip import synth
@@ -118,16 +119,18 @@ def test_window_matvec(kind, tokens, tables, dev):
     assert torch.equal(alone, got)
 
 
-@pytest.mark.parametrize("kind", ["Q2_0", "IQ4_XS", "IQ1_M"])
-def test_matvec_separate(kind, tables, dev):
+@pytest.mark.parametrize("kind", ["Q2_0", "IQ4_XS", "IQ1_M", "IQ3_S"])
+@pytest.mark.parametrize("dtype", ["float32", "bfloat16", "float16"])
+def test_matvec_separate(kind, dtype, tables, dev):
     E, R, C = 4, 24, 512
     raw, w = stack(kind, E, R, C, 10, tables)
     per = len(raw) // E
     experts = [torch.from_numpy(raw[e * per:(e + 1) * per].copy()).to(dev) for e in (2, 0, 3, 3)]
     rng = np.random.default_rng(11)
-    x, xv = act(rng, (2, C), "float32")
+    x, xv = act(rng, (2, C), dtype)
     got = SB.matvec_separate(experts, kind, R, C, x.to(dev), 2).cpu()
-    assert rel_err(got, OB.matvec(w, np.array([2, 0, 3, 3]), xv, 2)) <= 1e-5
+    assert got.dtype == TORCH[dtype]
+    assert rel_err(got.float(), OB.matvec(w, np.array([2, 0, 3, 3]), xv, 2)) <= TOL[dtype]
 
 
 @pytest.mark.parametrize("kind", ["Q2_0", "IQ3_S", "IQ2_XS"])
@@ -158,6 +161,50 @@ def test_the_glu_table_built_in_down_gives_the_bits_of_its_own_kernel(pairs, row
     got = SB.lookup_down_glu(down, idx, gate, up)
     assert got is not None and got.dtype == torch.float16
     assert torch.equal(got, SB.lookup_matvec(down, idx, SB.lookup_table_glu(gate, up), 1))
+
+
+@pytest.mark.parametrize("dtype", ["float16", "bfloat16"])
+def test_lookup_table_is_the_oracles_bit_for_bit(dtype, dev):
+    rng = np.random.default_rng(16)
+    x, xv = act(rng, (3, 640), dtype)
+    got = SB.lookup_table(x.to(dev)).float().cpu().numpy()
+    np.testing.assert_array_equal(got, OL.lookup_table(xv, dtype))
+
+
+@pytest.mark.parametrize("cols", [512, 640])
+@pytest.mark.parametrize("share", [1, 2])
+def test_lookup_matvec_is_the_oracles_table_product(cols, share, tables, dev):
+    """The table's float16 rounding modelled (blocks.py:595-603, 618-643): only the float32 sums' order and the
+    output's rounding are left."""
+    E, R = 3, 64
+    raw, _ = stack("Q2_0", E, R, cols, 17, tables)
+    lin = SB.BlockSwitchLinear(torch.from_numpy(raw).to(dev), "Q2_0", (E, R, cols))
+    rng = np.random.default_rng(18)
+    idx = np.array([0, 2, 1, 1, 2, 0])
+    x, xv = act(rng, (len(idx) // share, cols), "float16")
+    got = SB.lookup_matvec(lin, torch.from_numpy(idx).to(dev), SB.lookup_table(x.to(dev)), share).float().cpu().numpy()
+    want = OL.lookup_matvec(raw, (E, R, cols), idx, OL.lookup_table(xv, "float16"), share)
+    assert (np.abs(got - want) <= 2.0 ** -11 * np.abs(want) + 1e-6 * np.abs(want).max()).all()
+
+
+@pytest.mark.parametrize("pairs", [1, 10])
+def test_lookup_down_glu_is_the_oracles(pairs, tables, dev):
+    """silu(gate) * up in float32 into the float16 table (blocks.py:606-616, 702-760); the exponential's last bit
+    may move an entry by one float16 step."""
+    E, R, C = 3, 96, 640
+    raw, _ = stack("Q2_0", E, R, C, 19, tables)
+    down = SB.BlockSwitchLinear(torch.from_numpy(raw).to(dev), "Q2_0", (E, R, C))
+    rng = np.random.default_rng(20 + pairs)
+    idx = rng.integers(0, E, pairs)
+    g, gv = act(rng, (pairs, C), "float16")
+    u, uv = act(rng, (pairs, C), "float16")
+    tab = SB.lookup_table_glu(g.to(dev), u.to(dev)).float().cpu().numpy()
+    want_tab = OL.lookup_table_glu(gv, uv, "float16")
+    step = np.abs(want_tab) * 2.0 ** -10 + 2.0 ** -24
+    assert (np.abs(tab - want_tab) <= step).all() and (tab == want_tab).mean() > 0.99
+    got = SB.lookup_down_glu(down, torch.from_numpy(idx).to(dev), g.to(dev), u.to(dev)).float().cpu().numpy()
+    want = OL.lookup_down_glu(raw, (E, R, C), idx, gv, uv, "float16")
+    assert rel_err(got, want) <= 2e-3
 
 
 def test_lookup_matvec_is_the_product(tables, dev):

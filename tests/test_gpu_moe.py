@@ -206,3 +206,39 @@ def test_the_benchmark_shape_with_few_groups(tokens, k, dtype, c3_layers, tables
     assert rel_err(out.float().cpu(), want) <= 1e-2
     for _ in range(2):
         assert torch.equal(moe(logits.to(dev), x.to(dev)), out)
+
+
+@pytest.mark.parametrize("kinds", [("Q2_0", "Q2_0"), ("IQ3_S", "IQ3_S")])
+@pytest.mark.parametrize("tokens", [2, 3, 4])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_the_tails_own_combine_gives_the_combine_kernels_bits(kinds, tokens, dtype, c3_layers, tables, dev):
+    """Windows of 2-4 tokens combine in the down kernel (its last block of a row tile, after a release / acquire
+    hand-off of the routed outputs between blocks); larger ones in a combine kernel after it. The same inputs both
+    ways give the same bits, call after call."""
+    from strata_hip import _lib
+
+    E, D, F, K = 512, 2048, 512, 10
+    fetch, lin, shared = c3_layers[kinds]
+    rng = np.random.default_rng(tokens + 300)
+    x = torch.from_numpy(rng.standard_normal((tokens, D)).astype(np.float32)).to(dtype).to(dev)
+    logits = torch.from_numpy(rng.standard_normal((tokens, E)).astype(np.float32)).to(dtype).to(dev)
+    wg = torch.from_numpy(rng.standard_normal(D).astype(np.float32) * 0.05).to(dtype).to(dev)
+    moe = SF.MoEDecode(lin["gate"], lin["up"], lin["down"], lin["sgate"], lin["sup"], lin["sdown"], wg, K)
+    lib = _lib.load()
+    before = lib.sh_moe_set_tail_combine(16)
+    try:
+        in_tail = moe(logits, x)
+        torch.cuda.synchronize()
+        lib.sh_moe_set_tail_combine(0)
+        separate = moe(logits, x)
+        torch.cuda.synchronize()
+        assert torch.equal(in_tail, separate)
+        lib.sh_moe_set_tail_combine(16)
+        for _ in range(2):
+            assert torch.equal(moe(logits, x), in_tail)
+    finally:
+        lib.sh_moe_set_tail_combine(before)
+    name = "bfloat16" if dtype == torch.bfloat16 else "float16"
+    want, _, _ = OM.moe_decode_blocks(logits.float().cpu().numpy(), x.float().cpu().numpy(), K, fetch, kinds,
+                                      (E, D, F), shared, wg.float().cpu().numpy(), tables, name)
+    assert rel_err(in_tail.float().cpu(), want) <= 1e-2
