@@ -137,14 +137,26 @@ int sh_tiles_of(const int32_t* idx, int64_t pairs, int64_t k, int64_t experts, i
  * operands) two kernels (route + gate/up + SwiGLU; down + combine), otherwise three (route; gate/up; down +
  * combine). kind / kind_down: Q2_0 or IQ3_S; dtype: F16 or BF16; d_model, d_ff multiples of 256; experts a multiple
  * of 64 up to 2048. idx_out (tokens x k int32) and w_out (tokens x k float32) are optional copies of the choice.
- * workspace: sh_moe_workspace() bytes, zeroed once before its first call (it holds counters that every call leaves
- * at zero); calls sharing a workspace must not overlap. */
+ * workspace: sh_moe_workspace() bytes; nothing in it has to start at zero (each call clears what it counts in);
+ * calls sharing a workspace must not overlap. */
 size_t sh_moe_workspace(int64_t tokens, int64_t k, int64_t d_model, int64_t d_ff, int dtype);
 int sh_moe_decode(int kind, int kind_down, const void* gate, const void* up, const void* down, int64_t experts,
                   const void* shared_gate, const void* shared_up, const void* shared_down, const void* shared_gate_w,
                   const void* tables, const void* logits, int logits_dtype, const void* x, int dtype, int64_t tokens,
                   int64_t k, int64_t d_model, int64_t d_ff, void* out, int32_t* idx_out, float* w_out,
                   void* workspace, size_t workspace_bytes, void* stream);
+/* No counterpart in the reference: sh_moe_decode for callers that cannot allocate (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc). The same arguments without the workspace: the library's
+ * own device array of sh_moe_scratch_bytes() (8 MiB) on each GPU serves as it, found once per device at the first
+ * call there. Nothing is allocated. Shapes whose workspace (sh_moe_workspace) exceeds the array are refused with
+ * SH_E_WORKSPACE before anything is launched. Every call on a GPU shares that GPU's array: calls that overlap on one
+ * GPU (two streams, two threads) race and must be ordered by the caller. */
+size_t sh_moe_scratch_bytes(void);
+int sh_moe_decode_noalloc(int kind, int kind_down, const void* gate, const void* up, const void* down,
+                          int64_t experts, const void* shared_gate, const void* shared_up, const void* shared_down,
+                          const void* shared_gate_w, const void* tables, const void* logits, int logits_dtype,
+                          const void* x, int dtype, int64_t tokens, int64_t k, int64_t d_model, int64_t d_ff,
+                          void* out, int32_t* idx_out, float* w_out, void* stream);
 /* No counterpart in the reference (a tuning knob for callers and tests): windows of at most `upto` tokens (0..16)
  * have the routed outputs combined by the down kernel's last block of each row tile, larger ones by a combine kernel
  * after it (default 4). Both give the same bits. Returns the previous bound. Process-wide; not for use while

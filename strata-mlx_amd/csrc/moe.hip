@@ -17,6 +17,7 @@
 // order its MFMA fragments take them, and are read straight from memory (L2). Grids are sized by the most groups
 // there could be (B*k + 1); blocks past the groups the route found leave at once, so nothing waits on the host.
 #include <atomic>
+#include <mutex>
 
 #include "launch.h"
 #include "regmac.h"
@@ -1326,9 +1327,61 @@ int moe_decode(int phases, int kind, int kind_down, const void* gate, const void
   return OK;
 }
 
+// ---- the entry point that allocates nothing: its workspace is this file's device array, one copy a GPU
+
+constexpr size_t MOE_SCRATCH_BYTES = (size_t)8 << 20;
+static __device__ __align__(256) uint8_t scratch[MOE_SCRATCH_BYTES];
+
+constexpr int MAX_DEVICES = 64;
+static std::mutex g_scratch_mu;
+static void* g_scratch_at[MAX_DEVICES];  // the array's device address on each GPU, found once a GPU
+
+// the current device's copy of `scratch`: its address comes from the runtime (the array's name in host code is a
+// stand-in, not a device address), looked up the first time a device calls and kept for it
+static int scratch_of(void** at) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= MAX_DEVICES)
+    return fail(E_HIP, "moe_decode_noalloc: no current device (%d)", dev);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_at[dev]) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+      return fail(E_HIP, "moe_decode_noalloc: address of the scratch array on device %d: %s", dev,
+                  hipGetErrorString(e));
+    g_scratch_at[dev] = p;
+  }
+  *at = g_scratch_at[dev];
+  return OK;
+}
+
 }  // namespace
 
 extern "C" {
+
+size_t sh_moe_scratch_bytes(void) { return MOE_SCRATCH_BYTES; }
+
+int sh_moe_decode_noalloc(int kind, int kind_down, const void* gate, const void* up, const void* down,
+                          int64_t experts, const void* shared_gate, const void* shared_up, const void* shared_down,
+                          const void* shared_gate_w, const void* tables, const void* logits, int logits_dtype,
+                          const void* x, int dtype, int64_t tokens, int64_t k, int64_t d_model, int64_t d_ff,
+                          void* out, int32_t* idx_out, float* w_out, void* stream) {
+  if (tokens > 0 && k > 0 && d_model > 0 && d_ff > 0) {
+    const size_t need = moe_carve(nullptr, nullptr, tokens, k, d_model, d_ff, dtype_size(dtype));
+    if (need > MOE_SCRATCH_BYTES)
+      return fail(E_WORKSPACE, "moe_decode_noalloc: %lld tokens x %lld experts at d_model %lld, d_ff %lld need %zu "
+                  "bytes of scratch; the library's array holds %zu", (long long)tokens, (long long)k,
+                  (long long)d_model, (long long)d_ff, need, MOE_SCRATCH_BYTES);
+  }
+  if (tokens <= 0) return OK;
+  void* ws = nullptr;
+  const int st = scratch_of(&ws);
+  if (st) return st;
+  // nothing in the workspace has to start at zero: the first kernel of each call clears the tail's counters
+  return moe_decode(7, kind, kind_down, gate, up, down, experts, shared_gate, shared_up, shared_down, shared_gate_w,
+                    tables, logits, logits_dtype, x, dtype, tokens, k, d_model, d_ff, out, idx_out, w_out, ws,
+                    MOE_SCRATCH_BYTES, stream);
+}
 
 size_t sh_moe_workspace(int64_t tokens, int64_t k, int64_t d_model, int64_t d_ff, int dtype) {
   if (tokens <= 0 || k <= 0 || d_model <= 0 || d_ff <= 0) return 0;

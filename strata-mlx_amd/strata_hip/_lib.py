@@ -46,6 +46,9 @@ PROTOTYPES = {
     "sh_moe_decode_phase": [c_int, c_int, c_int, c_vp, c_vp, c_vp, c_i64, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_int,
                             c_vp, c_int, c_i64, c_i64, c_i64, c_i64, c_vp, c_vp, c_sz, c_vp],
     "sh_moe_set_tail_combine": [c_int],
+    "sh_moe_scratch_bytes": [],
+    "sh_moe_decode_noalloc": [c_int, c_int, c_vp, c_vp, c_vp, c_i64, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_int, c_vp,
+                              c_int, c_i64, c_i64, c_i64, c_i64, c_vp, c_vp, c_vp, c_vp],
     "sh_tile_matmul": [c_int, c_vp, c_vp, c_i64, c_i64, c_i64, c_vp, c_int, c_i64, c_vp, c_vp, c_vp],
     "sh_tile_glu": [c_int, c_vp, c_vp, c_vp, c_i64, c_i64, c_i64, c_vp, c_int, c_i64, c_vp, c_i64, c_vp, c_vp,
                     c_vp],
@@ -60,7 +63,7 @@ PROTOTYPES = {
 _RESTYPE = {"sh_last_error": ctypes.c_char_p, "sh_tables_bytes": c_sz, "sh_tiles_workspace": c_sz,
             "sh_tiles_most": c_i64, "sh_switch_workspace": c_sz,
             "sh_moe_workspace": c_sz, "sh_stack_workspace": c_sz, "sh_paged_attn_workspace": c_sz,
-            "sh_cells_attn_workspace": c_sz}
+            "sh_cells_attn_workspace": c_sz, "sh_moe_scratch_bytes": c_sz}
 
 _lib = None
 

@@ -139,6 +139,30 @@ class MoEDecode:
             self._ws[key] = torch.zeros(n, dtype=torch.uint8, device=device)
         return self._ws[key]
 
+    def decode_into(self, logits: torch.Tensor, x: torch.Tensor, out: torch.Tensor, idx: torch.Tensor | None = None,
+                    w: torch.Tensor | None = None) -> torch.Tensor:
+        """The decode step into the caller's `out` (and optional idx int32 / w float32 of the choice) with nothing
+        allocated: the library's own scratch array stands in for the workspace (sh_moe_decode_noalloc). For code
+        under graph capture or loops that must not allocate; calls on one GPU must not overlap. Inputs and outputs
+        contiguous."""
+        tokens = x.numel() // self.d_model
+        if not self.takes(x):
+            raise ValueError(f"MoEDecode: {tokens} tokens of {x.dtype} (at most {self.MAX_TOKENS}, bf16/fp16)")
+        for t in (logits, x, out) + tuple(a for a in (idx, w) if a is not None):
+            if not t.is_contiguous():
+                raise ValueError("decode_into: contiguous tensors expected")
+        if out.numel() != x.numel() or out.dtype != x.dtype:
+            raise ValueError(f"decode_into: out of {tuple(out.shape)} {out.dtype} for x of {tuple(x.shape)} {x.dtype}")
+        needs = self.gate.kind == "IQ3_S" or self.down.kind == "IQ3_S"
+        tabs = _tables.device_blob(x.device).data_ptr() if needs else None
+        sg, su, sd = self.shared
+        _lib.call("sh_moe_decode_noalloc", self.kinds[0], self.kinds[1], self.gate.blocks.data_ptr(),
+                  self.up.blocks.data_ptr(), self.down.blocks.data_ptr(), self.experts, sg.blocks.data_ptr(),
+                  su.blocks.data_ptr(), sd.blocks.data_ptr(), self.shared_gate_w.data_ptr(), tabs, logits.data_ptr(),
+                  _lib.dtype_code(logits.dtype), x.data_ptr(), _lib.dtype_code(x.dtype), tokens, self.k, self.d_model,
+                  self.d_ff, out.data_ptr(), _lib.ptr(idx), _lib.ptr(w), _lib.stream_of(x))
+        return out
+
     def __call__(self, logits: torch.Tensor, x: torch.Tensor, want_choice: bool = False, phase: int | None = None,
                  out: torch.Tensor | None = None):
         """logits (..., experts) float32 or x's type; x (..., d_model). Returns (..., d_model) in x's type, and the
