@@ -182,17 +182,30 @@ int sh_tile_matmul(int kind, const void* blocks, const void* tables, int64_t exp
  * .astype(x.dtype)) in one pass: h[s] = x_dtype(silu(g) * u), g / u = gate / up of tile_expert[s / 16] . x[token[s]]
  * with the weights rounded to x's type and float32 sums. gate and up: stacks of `experts` (rows, cols) layers of
  * Q2_0 or IQ3_S; x (tokens, cols) bfloat16 / float16; token, h: `slots` (a multiple of 16) entries / rows; rows
- * % 32 == 0, cols % 256 == 0. Tokens outside 0..tokens-1 are clamped; tiles naming no expert leave their rows. */
+ * % 32 == 0, cols % 64 == 0. Tokens outside 0..tokens-1 are clamped; tiles naming no expert leave their rows. */
 int sh_tile_glu(int kind, const void* gate, const void* up, const void* tables, int64_t experts, int64_t rows,
                 int64_t cols, const void* x, int x_dtype, int64_t tokens, const int32_t* token, int64_t slots,
                 const int32_t* tile_expert, void* h, void* stream);
 
 /* strata_mlx/blocks.py:575 (out = tile_matmul(down, h)[where].astype(x.dtype)) in one pass: for each slot s with
  * pair[s] in 0..pairs-1, out[pair[s]] = h_dtype(down of tile_expert[s / 16] . h[s]) (pair = the inverse of
- * tiles_of's `where`, -1 for slots no pair fills). down: Q2_0 or IQ3_S, rows % 64 == 0, cols % 256 == 0. */
+ * tiles_of's `where`, -1 for slots no pair fills). down: Q2_0 or IQ3_S, rows % 64 == 0, cols % 64 == 0. */
 int sh_tile_down(int kind, const void* down, const void* tables, int64_t experts, int64_t rows, int64_t cols,
                  const void* h, int h_dtype, int64_t slots, const int32_t* tile_expert, const int32_t* pair,
                  int64_t pairs, void* out, void* stream);
+
+/* ---- dense layers: Q6_K held as three parts (strata_mlx/dense.py:109-167, ScaledLinear), w[r][c] = code[r][c] *
+ * scale[r][c / 16] * d[r][c / d_step]: codes int8 (rows, cols), scales int8 (rows, cols / 16), d float16 (rows,
+ * cols / d_step); rows % 4 == 0, cols % 256 == 0, d_step a multiple of 16 dividing cols. */
+
+/* dense.py:149-167 (ScaledLinear.__call__ for a window): out[t] = W . x[t] for tokens <= 8, x and out in x_dtype
+ * (F32, F16 or BF16), float32 sums. */
+int sh_scaled_matvec(const int8_t* codes, const int8_t* scales, const uint16_t* d, int64_t rows, int64_t cols,
+                     int64_t d_step, const void* x, int x_dtype, int64_t tokens, void* out, void* stream);
+/* dense.py:120-135 (ScaledLinear.floats, kernel _FLOATS 72-82): every weight worked out in float32 and rounded
+ * once to out_dtype, (rows, cols). */
+int sh_scaled_floats(const int8_t* codes, const int8_t* scales, const uint16_t* d, int64_t rows, int64_t cols,
+                     int64_t d_step, void* out, int out_dtype, void* stream);
 
 /* ---- decode attention (strata_mlx/attention.py:118-165) */
 

@@ -93,7 +93,7 @@ __global__ __launch_bounds__(TG * 64) void k_tile_matmul(const uint8_t* __restri
   const int t0 = blockIdx.x * TG, r0 = blockIdx.y * RB;
   const int nt = min(TG, n_tiles - t0);
   const int slab = RB * (int)rbytes;  // bytes of the run's rows: contiguous in the stack
-  const int nch = cols / KCH;
+  const int nch = (cols + KCH - 1) / KCH;  // the last chunk may be partial: whole runs of 32 past the row are zeros
 
   if constexpr (KIND == IQ3_S) {
     for (int i = tid; i < IQ3S_SIGNED_BYTES / 16; i += NT) ((u32x4*)tab)[i] = ((const u32x4*)(tables + TAB_IQ3S_SIGNED))[i];
@@ -138,8 +138,9 @@ __global__ __launch_bounds__(TG * 64) void k_tile_matmul(const uint8_t* __restri
     }
     __syncthreads();
     auto dequant = [&](int c, int buf) {
-      u32x4 w[4];
-      dequant_run<KIND, XT>(raw + ur * (int)rbytes, c * (KCH / 32) + urun, tab, w);
+      u32x4 w[4] = {};
+      const int run = c * (KCH / 32) + urun;
+      if (run * 32 < cols) dequant_run<KIND, XT>(raw + ur * (int)rbytes, run, tab, w);
       XT* dst = wl + buf * RB * KCH + ur * KCH;
 #pragma unroll
       for (int q = 0; q < 4; ++q) *(u32x4*)(dst + 8 * ((4 * urun + q) ^ (ur & SW))) = w[q];
@@ -153,7 +154,8 @@ __global__ __launch_bounds__(TG * 64) void k_tile_matmul(const uint8_t* __restri
       u32x4 af[KCH / 32];
       if (mine) {
 #pragma unroll
-        for (int ks = 0; ks < KCH / 32; ++ks) af[ks] = *(const u32x4*)(arow + c * KCH + ks * 32 + 8 * g);
+        for (int ks = 0; ks < KCH / 32; ++ks)
+          af[ks] = c * KCH + ks * 32 < cols ? *(const u32x4*)(arow + c * KCH + ks * 32 + 8 * g) : u32x4{0u, 0u, 0u, 0u};
       }
       __syncthreads();  // chunk c is in buffer c & 1; chunk c - 1's readers are done with the other
       if (c + 1 < nch) dequant(c + 1, (c + 1) & 1);
@@ -195,7 +197,7 @@ static int launch_tiles(const uint8_t* blocks, const uint8_t* tables, int64_t ex
 }
 
 
-// ---- the streaming form (Q2_0 and IQ3_S, columns in chunks of 256, rows in blocks of 64)
+// ---- the streaming form (Q2_0 and IQ3_S, columns in chunks of 256, the last possibly partial, rows in blocks of 64)
 //
 // Persistent blocks, one a CU. A block first lays its window of tiles out in units: a unit is at most TS_TGU
 // consecutive tiles of one expert, a run of one expert's tiles cut every TS_TGU tiles from its start; tiles that
@@ -295,7 +297,9 @@ __global__ __launch_bounds__(TS_NT) void k_tile_stream(TileStreamArgs g) {
 
   const int tid = threadIdx.x, lane = tid & 63, n = lane & 15, gq = lane >> 4;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int nch = g.cols / TS_KCH, rblk = g.rows / VR;
+  // the last chunk may be partial (Q2_0 rows of 64-column blocks): its bytes past the row are not loaded, its runs
+  // past the row dequantize to zeros and its activations past the row are zeros
+  const int nch = (g.cols + TS_KCH - 1) / TS_KCH, rblk = g.rows / VR;
   const int64_t rbytes = g.rbytes;
 
   if constexpr (KIND == IQ3_S) {  // the signed table, once a block
@@ -409,7 +413,8 @@ __global__ __launch_bounds__(TS_NT) void k_tile_stream(TileStreamArgs g) {
       auto issue = [&]() {  // chunk ci.q into ring slot islot: piece j of row v
         const uint8_t* src = ibase + ci.c * CB;
         const int lead = (int)((uintptr_t)src & 15);
-        if (16 * j < lead + CB) lds_dma16p(src - lead + 16 * j, ring_lds + (uint32_t)(islot * TS_SLOT + wave * 1024));
+        const int cb = min(CB, (int)rbytes - ci.c * CB);  // the chunk's bytes in the row
+        if (16 * j < lead + cb) lds_dma16p(src - lead + 16 * j, ring_lds + (uint32_t)(islot * TS_SLOT + wave * 1024));
         islot = islot + 1 == TS_NR ? 0 : islot + 1;
         cur_next(ci);
         if (ci.c == 0 && ci.q < Q) ibase = row_base(ci);
@@ -417,8 +422,8 @@ __global__ __launch_bounds__(TS_NT) void k_tile_stream(TileStreamArgs g) {
       auto dequant = [&]() {  // chunk cd.q into buffer cd.q & 1: run j of row v
         const uint8_t* src = dbase + cd.c * CB;
         const uint8_t* raw = ring + dslot * TS_SLOT + v * (TS_PPR * 16) + ((uintptr_t)src & 15);
-        u32x4 w[4];
-        dequant_run<KIND, XT>(raw, j, tab, w);
+        u32x4 w[4] = {};
+        if (cd.c * TS_KCH + 32 * j < g.cols) dequant_run<KIND, XT>(raw, j, tab, w);
         XT* dst = wl + (cd.q & 1) * TS_BUF + v * TS_KCH;
 #pragma unroll
         for (int h = 0; h < 4; ++h) *(u32x4*)(dst + 8 * ((4 * j + h) ^ (v & 15))) = w[h];
@@ -483,9 +488,11 @@ __global__ __launch_bounds__(TS_NT) void k_tile_stream(TileStreamArgs g) {
           arow = a + row * g.cols;
         }
         if (cw < s.len) {
+          const int left = g.cols - s.c * TS_KCH;  // columns of the row from this chunk on
 #pragma unroll
           for (int ks = 0; ks < TS_KCH / 32; ++ks)
-            af[BUF][ks] = *(const u32x4*)(arow + s.c * TS_KCH + ks * 32 + 8 * gq);
+            af[BUF][ks] = ks * 32 < left ? *(const u32x4*)(arow + s.c * TS_KCH + ks * 32 + 8 * gq)
+                                         : u32x4{0u, 0u, 0u, 0u};
         } else {  // (defined on every path: the fragments are not live across the epilogue)
 #pragma unroll
           for (int ks = 0; ks < TS_KCH / 32; ++ks) af[BUF][ks] = u32x4{0u, 0u, 0u, 0u};
@@ -609,7 +616,6 @@ int sh_tile_matmul(int kind, const void* blocks, const void* tables, int64_t exp
   if (pairs <= 0) return OK;
   if (rows % RB || cols % 64) return fail(E_SHAPE, "tile_matmul: %lld x %lld is not in tiles of %d x 64",
                                           (long long)rows, (long long)cols, RB);
-  if (cols % KCH) return fail(E_UNSUPPORTED, "tile_matmul: %lld columns (a multiple of %d)", (long long)cols, KCH);
   if (pairs % TILE_TOKENS) return fail(E_SHAPE, "tile_matmul: %lld pairs are not whole tiles of 16", (long long)pairs);
   if (a_dtype != BF16 && a_dtype != F16)
     return fail(E_UNSUPPORTED, "tile_matmul: activations of dtype %d (bfloat16 or float16)", a_dtype);
@@ -655,9 +661,9 @@ int sh_tile_glu(int kind, const void* gate, const void* up, const void* tables, 
   if (st) return st;
   if (slots <= 0) return OK;
   if (kind != IQ3_S && kind != Q2_0) return fail(E_UNSUPPORTED, "tile_glu: kind %d (Q2_0 or IQ3_S)", kind);
-  if (rows % (TS_RBV / 2) || cols % TS_KCH)
-    return fail(E_UNSUPPORTED, "tile_glu: %lld x %lld is not in blocks of %d x %d", (long long)rows, (long long)cols,
-                TS_RBV / 2, TS_KCH);
+  if (rows % (TS_RBV / 2) || cols % 64)
+    return fail(E_UNSUPPORTED, "tile_glu: %lld x %lld is not in blocks of %d x 64", (long long)rows, (long long)cols,
+                TS_RBV / 2);
   if (slots % TILE_TOKENS) return fail(E_SHAPE, "tile_glu: %lld slots are not whole tiles of 16", (long long)slots);
   if (slots / TILE_TOKENS > (1 << 26) || tokens <= 0)
     return fail(E_SHAPE, "tile_glu: %lld slots of %lld tokens", (long long)slots, (long long)tokens);
@@ -684,9 +690,9 @@ int sh_tile_down(int kind, const void* down, const void* tables, int64_t experts
   if (st) return st;
   if (slots <= 0 || pairs <= 0) return OK;
   if (kind != IQ3_S && kind != Q2_0) return fail(E_UNSUPPORTED, "tile_down: kind %d (Q2_0 or IQ3_S)", kind);
-  if (rows % TS_RBV || cols % TS_KCH)
-    return fail(E_UNSUPPORTED, "tile_down: %lld x %lld is not in blocks of %d x %d", (long long)rows,
-                (long long)cols, TS_RBV, TS_KCH);
+  if (rows % TS_RBV || cols % 64)
+    return fail(E_UNSUPPORTED, "tile_down: %lld x %lld is not in blocks of %d x 64", (long long)rows,
+                (long long)cols, TS_RBV);
   if (slots % TILE_TOKENS) return fail(E_SHAPE, "tile_down: %lld slots are not whole tiles of 16", (long long)slots);
   if (slots / TILE_TOKENS > (1 << 26)) return fail(E_SHAPE, "tile_down: %lld slots", (long long)slots);
   if (!down || (kind == IQ3_S && !tables) || !h || !tile_expert || !pair || !out)

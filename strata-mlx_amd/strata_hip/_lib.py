@@ -49,6 +49,8 @@ PROTOTYPES = {
     "sh_moe_scratch_bytes": [],
     "sh_moe_decode_noalloc": [c_int, c_int, c_vp, c_vp, c_vp, c_i64, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_int, c_vp,
                               c_int, c_i64, c_i64, c_i64, c_i64, c_vp, c_vp, c_vp, c_vp],
+    "sh_scaled_matvec": [c_vp, c_vp, c_vp, c_i64, c_i64, c_i64, c_vp, c_int, c_i64, c_vp, c_vp],
+    "sh_scaled_floats": [c_vp, c_vp, c_vp, c_i64, c_i64, c_i64, c_vp, c_int, c_vp],
     "sh_tile_matmul": [c_int, c_vp, c_vp, c_i64, c_i64, c_i64, c_vp, c_int, c_i64, c_vp, c_vp, c_vp],
     "sh_tile_glu": [c_int, c_vp, c_vp, c_vp, c_i64, c_i64, c_i64, c_vp, c_int, c_i64, c_vp, c_i64, c_vp, c_vp,
                     c_vp],

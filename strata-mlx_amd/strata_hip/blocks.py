@@ -216,16 +216,19 @@ class BlockSwitchLinear:
         return out.reshape(*ishape, 1, self.output_dims)
 
     def _as_floats(self, x: torch.Tensor, indices: torch.Tensor) -> torch.Tensor:
-        """Many pairs of a shape the tiles do not take: the stack unpacked once, each expert's pairs multiplied
-        by torch's GEMM (the reference's gather_mm route, strata_mlx/blocks.py:438-440)."""
-        w = dequantize(self.blocks, self.kind, self.shape, x.dtype)
+        """Many pairs of a shape the tiles of switch_glu did not take. The reference unpacks the stack to x's type
+        and multiplies with gather_mm (strata_mlx/blocks.py:438-440): the same roundings here, the pairs laid out
+        in tiles of one expert and multiplied by the grouped GEMM (weights rounded to x's type, float32 sums, the
+        result in x's type). Shapes the tiles do not take go through the expert matvec."""
         ishape = tuple(indices.shape)
-        flat = indices.reshape(-1).long()
         xs = torch.broadcast_to(x, (*ishape, 1, self.input_dims)).reshape(-1, self.input_dims)
-        out = torch.empty((flat.numel(), self.output_dims), dtype=x.dtype, device=x.device)
-        for e in torch.unique(flat).tolist():
-            rows = (flat == e).nonzero().reshape(-1)
-            out[rows] = (xs[rows].float() @ w[e].float().T).to(x.dtype)
+        flat = indices.reshape(-1)
+        if tileable(self.kind, self.output_dims, self.input_dims):
+            te, token, where = tiles_of(flat[:, None], self.num_experts)
+            out = tile_matmul(self.blocks, self.kind, self.shape, xs[token.long()], te)[where.long()].to(x.dtype)
+        else:
+            out = torch.cat([switch_matvec(self.blocks, self.kind, self.shape, flat[a:a + 65535], xs[a:a + 65535], 1)
+                             for a in range(0, flat.numel(), 65535)])
         return out.reshape(*ishape, 1, self.output_dims)
 
 
@@ -324,10 +327,13 @@ def _lookup_glu(x, indices, up, gate, down):
 # ---- prompts: pairs in tiles of one expert, under MFMA (tiles.hip)
 
 def tileable(kind: str, rows: int, cols: int) -> bool:
-    """Whether `tile_matmul` takes a stack of such layers (strata_mlx/blocks.py:511-513): the reference's rule
-    (rows % 64, cols % 64, whole blocks), with columns in whole chunks of 256. Q2_0 and IQ3_S stream their rows
-    through LDS chunk by chunk; the other kinds keep a row group of 64 rows in LDS beside the chunk buffers."""
-    if rows % ROWS_TILE or cols % COLS_TILE or cols % BLOCK[kind][0] or cols % 256:
+    """Whether `tile_matmul` takes a stack of such layers: the reference's rule (strata_mlx/blocks.py:511-513:
+    rows % 64, cols % 64, whole blocks). The kernels take columns in chunks of 256, the last one partial where the
+    row ends earlier. Q2_0 and IQ3_S stream their rows through LDS chunk by chunk; the other kinds keep a row group
+    of 64 rows in LDS beside the chunk buffers and their codebooks, so their rows must fit there too: IQ4_NL up to
+    2,240 weights, IQ4_XS up to 2,304 (at 2,560 the reference tiles them and this answers False: those prompts take
+    the expert matvec, with exact weights instead of weights rounded to the activations' type)."""
+    if rows % ROWS_TILE or cols % COLS_TILE or cols % BLOCK[kind][0]:
         return False
     if kind in STREAMED:
         return True

@@ -11,14 +11,16 @@ ROUTER_AS_IS = True  # fused.py:421
 COMBINE_UPTO = 65535  # tokens a combine call takes (the reference stops at 16, what it checked against MLX)
 
 
-class WindowLinear:
+class WindowLinear(torch.nn.Module):
     """A float16 / bfloat16 linear layer without bias whose products come back in float32, reading its weights as
-    they are for a window of up to 8 tokens (strata_mlx/fused.py:357-390). `linear` is anything with a `weight`
-    (rows, cols) tensor; longer inputs go through torch's matmul in float32."""
+    they are for a window of up to 8 tokens (strata_mlx/fused.py:357-390). `linear` is the model's layer (anything
+    with a `weight` (rows, cols) tensor); longer inputs, or weights of other types, go through the layer itself as
+    in the reference (`self.linear(x)`), or, for a layer that cannot be called, a float32 product."""
 
     upto = 8
 
     def __init__(self, linear):
+        super().__init__()
         self.linear = linear
         self.rows, self.cols = linear.weight.shape
 
@@ -29,9 +31,11 @@ class WindowLinear:
     def takes(self, x: torch.Tensor) -> bool:
         return x.numel() // self.cols <= self.upto and self.weight.dtype in (torch.float16, torch.bfloat16)
 
-    def __call__(self, x: torch.Tensor) -> torch.Tensor:
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
         tokens = x.numel() // self.cols
         if not self.takes(x):
+            if callable(self.linear):
+                return self.linear(x)
             return (x.reshape(-1, self.cols).float() @ self.weight.float().T).reshape(*x.shape[:-1], self.rows)
         xs = x.reshape(tokens, self.cols).contiguous()
         w = self.weight.contiguous()
@@ -76,22 +80,36 @@ def moe_combine(y: torch.Tensor, w: torch.Tensor, g: torch.Tensor, s: torch.Tens
     return out.reshape(*lead, d)
 
 
-class Routed:
-    """The MoE block with the router's choice made by `top_k` and its end by `moe_combine`
-    (strata_mlx/fused.py:484-497, the drop-in for mlx-lm's SparseMoeBlock).
+class SwiGLUExpert:
+    """The shared expert as mlx-lm's MLP computes it: down(swiglu(gate(x), up(x))), each projection a layer of the
+    file's blocks (a BlockLinear, or anything called like `nn.Linear`)."""
 
-    gate: a WindowLinear (or anything returning float32 logits); switch_mlp: a BlockSwitchGLU; shared_expert: a
-    callable x -> (..., D); shared_expert_gate: a callable x -> (..., 1); top_k: experts a token."""
+    def __init__(self, gate_proj, up_proj, down_proj):
+        self.gate_proj, self.up_proj, self.down_proj = gate_proj, up_proj, down_proj
 
-    def __init__(self, gate, switch_mlp, shared_expert, shared_expert_gate, top_k: int):
-        self.gate, self.switch_mlp = gate, switch_mlp
-        self.shared_expert, self.shared_expert_gate = shared_expert, shared_expert_gate
-        self.top_k = top_k
+    def __call__(self, x: torch.Tensor) -> torch.Tensor:
+        from .blocks import swiglu
+
+        return self.down_proj(swiglu(self.gate_proj(x), self.up_proj(x)))
+
+
+FUSED = True  # windows the two-kernel decode takes go there (MoEDecode); False: always the composition
+
+
+class _RoutedCall:
+    """The MoE block's call with the router's choice made by `top_k` and its end by `moe_combine`
+    (strata_mlx/fused.py:484-497, `_Routed.__call__`), over the block's own attributes: gate, switch_mlp,
+    shared_expert, shared_expert_gate, top_k. A window the fused decode takes (routed experts as the file's Q2_0 /
+    IQ3_S blocks, the shared expert's projections too, a window of up to 16 tokens) runs as the router's product
+    and the two kernels of MoEDecode; any other as the reference composes it."""
 
     def __call__(self, x: torch.Tensor) -> torch.Tensor:
         gate = self.gate
         as_is = ROUTER_AS_IS and isinstance(gate, WindowLinear) and gate.takes(x)
         logits = gate(x if as_is else x.float())
+        fused = self._fused_for(x)
+        if fused is not None:
+            return fused(logits, x)
         idx, w = top_k(logits, self.top_k, weights=True)
         y = self.switch_mlp(x, idx)
         g, s = self.shared_expert_gate(x), self.shared_expert(x)
@@ -99,6 +117,61 @@ class Routed:
         if out is None:
             out = (y.float() * w[..., None]).sum(dim=-2).to(x.dtype) + torch.sigmoid(g.float()).to(x.dtype) * s
         return out
+
+    def _fused_for(self, x: torch.Tensor):
+        """The block's MoEDecode if it takes this window, else None (built once a block and activation type)."""
+        from .blocks import BlockSwitchGLU
+
+        if not FUSED or not isinstance(self.switch_mlp, BlockSwitchGLU):
+            return None
+        cache = self.__dict__.setdefault("_moe_decode", {})
+        key = (x.dtype, x.device)
+        if key not in cache:
+            cache[key] = None
+            sm, se = self.switch_mlp, self.shared_expert
+            parts = [getattr(se, n, None) for n in ("gate_proj", "up_proj", "down_proj")]
+            wg = getattr(self.shared_expert_gate, "weight", None)
+            if (all(hasattr(p, "blocks") and hasattr(p, "kind") for p in parts) and isinstance(wg, torch.Tensor)
+                    and wg.numel() == sm.gate_proj.input_dims and wg.dtype == x.dtype):
+                try:
+                    cache[key] = MoEDecode(sm.gate_proj, sm.up_proj, sm.down_proj, *parts, wg.reshape(-1), self.top_k)
+                except ValueError:
+                    cache[key] = None
+        moe = cache[key]
+        return moe if moe is not None and moe.takes(x) else None
+
+
+class _Routed(_RoutedCall):
+    """The MoE block as an object of its own (the reference swaps the class of mlx-lm's SparseMoeBlock instead:
+    `install_routers` does that here for blocks of any class)."""
+
+    def __init__(self, gate, switch_mlp, shared_expert, shared_expert_gate, top_k: int):
+        self.gate, self.switch_mlp = gate, switch_mlp
+        self.shared_expert, self.shared_expert_gate = shared_expert, shared_expert_gate
+        self.top_k = top_k
+
+
+Routed = _Routed
+_routed_classes = {}
+
+
+def install_routers(layers) -> None:
+    """Make the routers of `layers` products of this kind (WindowLinear), and their blocks' call `_Routed`'s
+    (strata_mlx/fused.py:500-507). A layer's `mlp` is taken when it has the MoE block's attributes; its class is
+    swapped for a subclass whose call is the routed one, so its parameters stay where they are."""
+    for layer in layers:
+        mlp = getattr(layer, "mlp", None)
+        if mlp is None or not all(hasattr(mlp, a) for a in ("gate", "switch_mlp", "shared_expert",
+                                                               "shared_expert_gate", "top_k")):
+            continue
+        if isinstance(getattr(mlp.gate, "weight", None), torch.Tensor) and not isinstance(mlp.gate, WindowLinear):
+            mlp.gate = WindowLinear(mlp.gate)
+        cls = type(mlp)
+        if not issubclass(cls, _RoutedCall):
+            if cls not in _routed_classes:
+                body = {"forward": _RoutedCall.__call__} if issubclass(cls, torch.nn.Module) else {}
+                _routed_classes[cls] = type(f"Routed{cls.__name__}", (_RoutedCall, cls), body)
+            mlp.__class__ = _routed_classes[cls]
 
 
 class MoEDecode:

@@ -3,8 +3,8 @@
 * Q2_0, Q3_K, IQ4_NL, IQ4_XS, IQ3_S: the affine form of strata_mlx/gguf.py:182-276 (`to_affine`), which reads the
   blocks as bit strings and words (little-endian bit order over the qh and sign bytes, 32-bit scale words with
   masks for Q3_K) where strata_mlx/blocks.py:57-194 (the oracle's text) indexes bytes.
-* IQ3_XXS, IQ2_S, IQ2_XS, IQ2_XXS, IQ1_M: ggml's published scalar dequantizers (ggml-quants `dequantize_row_*`,
-  as gguf-py 0.19.0 ports them), loops over 32-weight sub-blocks with their own indexing.
+* IQ3_XXS, IQ2_S, IQ2_XS, IQ2_XXS, IQ1_M, Q6_K: ggml's published scalar dequantizers (ggml-quants
+  `dequantize_row_*`, as gguf-py 0.19.0 ports them), loops over sub-blocks with their own indexing.
 
 Pure Python per block: slow, for a few blocks only. Returns float64 weights (exact).
 """
@@ -172,6 +172,28 @@ def iq1_m(b: bytes, t):  # ggml dequantize_row_iq1_m (grid values -1, 0, 1; the 
 
 DECODE = {"Q2_0": q2_0, "IQ4_NL": iq4_nl, "IQ4_XS": iq4_xs, "Q3_K": q3_k, "IQ3_S": iq3_s, "IQ3_XXS": iq3_xxs,
           "IQ2_S": iq2_s, "IQ2_XS": iq2_xs, "IQ2_XXS": iq2_xxs, "IQ1_M": iq1_m}
+
+
+def q6_k(b: bytes, t=None):  # ggml dequantize_row_q6_K: two halves of 128, four runs of 32 a half
+    ql, qh, sc = b[0:128], b[128:192], [x - 256 if x > 127 else x for x in b[192:208]]
+    d = f16(b[208:210])
+    y = [0.0] * 256
+    for half in range(2):
+        L, H, S, Y = 64 * half, 32 * half, 8 * half, 128 * half
+        for l in range(32):
+            s = l // 16
+            q1 = ((ql[L + l] & 15) | (((qh[H + l] >> 0) & 3) << 4)) - 32
+            q2 = ((ql[L + l + 32] & 15) | (((qh[H + l] >> 2) & 3) << 4)) - 32
+            q3 = ((ql[L + l] >> 4) | (((qh[H + l] >> 4) & 3) << 4)) - 32
+            q4 = ((ql[L + l + 32] >> 4) | (((qh[H + l] >> 6) & 3) << 4)) - 32
+            y[Y + l] = d * sc[S + s] * q1
+            y[Y + l + 32] = d * sc[S + s + 2] * q2
+            y[Y + l + 64] = d * sc[S + s + 4] * q3
+            y[Y + l + 96] = d * sc[S + s + 6] * q4
+    return y
+
+
+DECODE["Q6_K"] = q6_k
 
 
 def dequantize(blocks: np.ndarray, kind: str, block_bytes: int, tables) -> np.ndarray:
