@@ -220,6 +220,29 @@ int sh_paged_attn(const void* q, const void* k_pages, const void* v_pages, const
                   int64_t ctx_len, int64_t n_q, int64_t hq, int64_t hkv, int64_t head_dim, float scale, int dtype,
                   void* out, void* workspace, size_t workspace_bytes, void* stream);
 
+/* attention.py:261 (`o_proj(out * sigmoid(gate))`): sh_paged_attn with the output gate applied in the merge,
+ * out = T(T(out) * T(sigmoid(gate))); gate element (query t, head h, dim d) at gate[t * gate_token_stride + h *
+ * gate_head_stride + d], in `dtype` (the second half of each head of the q projection: stride 2 head_dim a head). */
+int sh_paged_attn_gated(const void* q, const void* k_pages, const void* v_pages, const int32_t* page_table,
+                        int64_t n_pages, int64_t ctx_len, int64_t n_q, int64_t hq, int64_t hkv, int64_t head_dim,
+                        float scale, int dtype, const void* gate, int64_t gate_token_stride, int64_t gate_head_stride,
+                        void* out, void* workspace, size_t workspace_bytes, void* stream);
+
+/* attention.py:183-222 (`qk_rope`, kernel _QK_ROPE 183-214): q or k of a window, x (tokens, heads, stride) with each
+ * head's head_dim values first: each head's rms norm with `weight` (head_dim) and eps, then rope on the first `rot`
+ * dims with cos / sin (tokens, rot), every step rounded to `dtype` as the reference's kernel does. out (heads,
+ * tokens, head_dim) when heads_first, else (tokens, heads, head_dim). head_dim a multiple of 64 up to 512. */
+int sh_qk_rope(const void* x, int dtype, int64_t tokens, int64_t heads, int64_t head_dim, int64_t stride,
+               const void* weight, float eps, const void* cos, const void* sin, int64_t rot, void* out, int heads_first,
+               void* stream);
+
+/* attention.py:251 (`cache.update_and_fetch(k, v)` of a paged cache): the window's keys and values k, v (n_new,
+ * hkv, head_dim) written at positions pos0 .. pos0 + n_new - 1, position p to page page_table[p / 16], slot p % 16
+ * of the pools (n_pages, hkv, 16, head_dim). Page ids outside 0..n_pages-1 are not written. Trimming rejected
+ * drafts is the caller's position count alone (the pages keep what they hold until written again). */
+int sh_kv_append(const void* k, const void* v, int64_t n_new, int64_t hkv, int64_t head_dim, int dtype, void* k_pages,
+                 void* v_pages, const int32_t* page_table, int64_t n_pages, int64_t pos0, void* stream);
+
 /* _gathered in its own form (attention.py:132-165): query s attends to the n_cells cells cells[s] (int32, rows of
  * k / v (hkv, kv_len, head_dim)) whose flag real[s] (uint8) is set; q (n_q, hq, head_dim) -> out (n_q, hq,
  * head_dim). workspace: sh_cells_attn_workspace() bytes. */
@@ -227,6 +250,15 @@ size_t sh_cells_attn_workspace(int64_t n_q, int64_t hq, int64_t hkv, int64_t hea
 int sh_cells_attn(const void* q, const void* k, const void* v, int64_t kv_len, const int32_t* cells,
                   const uint8_t* real, int64_t n_cells, int64_t n_q, int64_t hq, int64_t hkv, int64_t head_dim,
                   float scale, int dtype, void* out, void* workspace, size_t workspace_bytes, void* stream);
+
+/* attention.py:144-165 (`_gathered`) over a paged pool: the cells of sh_cells_attn (positions 0 .. n_pages * 16 - 1)
+ * read from pages (n_pages, hkv, 16, head_dim), position p at page page_table[p / 16], slot p % 16; `gate` (nullable)
+ * as in sh_paged_attn_gated. The attention entry's path for queries with an indexer's choice (attention.py:255-256). */
+int sh_cells_attn_paged(const void* q, const void* k_pages, const void* v_pages, const int32_t* page_table,
+                        int64_t n_pages, const int32_t* cells, const uint8_t* real, int64_t n_cells, int64_t n_q,
+                        int64_t hq, int64_t hkv, int64_t head_dim, float scale, int dtype, const void* gate,
+                        int64_t gate_token_stride, int64_t gate_head_stride, void* out, void* workspace,
+                        size_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus
 }

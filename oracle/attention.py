@@ -55,3 +55,37 @@ def gathered(q, k, v, cells, real, scale):
             o = sdpa(rows, ks, vs, np.broadcast_to(real[s], (H // G, cells.shape[1])), scale)
             out[0, s, g * (H // G) * D:(g + 1) * (H // G) * D] = o.reshape(-1)
     return out
+
+
+def qk_rope(x, w, cos, sin, heads, head_dim, stride, eps, dtype):
+    """attention.py:183-222 (`qk_rope`, kernel `_QK_ROPE`): x (S, heads * stride), each head's head_dim values first;
+    w (head_dim,); cos / sin (S, rot) -> (heads, S, head_dim) float32 values of `dtype`. Each head: rms norm (float32
+    sum of squares, 1 / sqrt(mean + eps)), normed = T(w * T(x * inv)); then for j < rot: a = T(v c), b = T(o s),
+    v = T(a + b) with o = -normed[j + rot/2] below rot/2, normed[j - rot/2] above."""
+    from .route import round_to
+
+    x = np.asarray(x, np.float32)
+    S = x.shape[0]
+    rot = np.asarray(cos).shape[-1]
+    xs = x.reshape(S, heads, stride)[..., :head_dim].astype(np.float64)
+    inv = 1.0 / np.sqrt((xs * xs).sum(axis=-1, keepdims=True) / head_dim + eps)
+    normed = round_to(np.asarray(w, np.float32) * round_to((xs * inv).astype(np.float32), dtype), dtype)
+    out = normed.copy()
+    if rot:
+        half = rot // 2
+        other = np.concatenate([-normed[..., half:rot], normed[..., :half]], axis=-1)
+        c = np.asarray(cos, np.float32)[:, None, :]
+        s = np.asarray(sin, np.float32)[:, None, :]
+        a = round_to((normed[..., :rot] * c).astype(np.float32), dtype)
+        b = round_to((other * s).astype(np.float32), dtype)
+        out[..., :rot] = round_to((a + b).astype(np.float32), dtype)
+    return out.transpose(1, 0, 2)
+
+
+def gate_out(out, gate, dtype):
+    """attention.py:261: out * sigmoid(gate), the sigmoid rounded to the type, then the product."""
+    from .route import round_to
+
+    g = np.asarray(gate, np.float64)
+    sig = round_to((1.0 / (1.0 + np.exp(-g))).astype(np.float32), dtype)
+    return round_to((round_to(out, dtype) * sig).astype(np.float32), dtype)

@@ -36,6 +36,10 @@ struct AttnArgs {
   int64_t kv_len;            // cells: rows of one KV head; paged: pages in the pool
   int tiles, tiles_per_split, splits, units, rows;  // rows: query rows of a unit (paged n_q * group, cells group)
   float scale_log2;          // scale * log2(e)
+  const void* gate;          // optional output gate: out = out * sigmoid(gate), gate element (query t, head h, dim d)
+  int64_t gate_ts, gate_hs;  // at gate[t * gate_ts + h * gate_hs + d]
+  const int32_t* cell_pages;  // cells over a paged pool: cell c at page cell_pages[c / 16], slot c % 16 (else null)
+  int64_t cell_npages;
 };
 
 constexpr int ATT_WAVES = 4, ATT_NT = 256;
@@ -97,7 +101,14 @@ __global__ __launch_bounds__(ATT_NT, 3) void k_attn_split(AttnArgs a) {  // (3 b
     const int32_t* src = CELLS ? a.table + (int64_t)qcell * a.ctx + 16 * t0 : a.table + t0;
     // ids outside the pool are clamped into it: a bad table gives wrong numbers, never a load outside K and V
     const int hi = (int)(a.kv_len - 1);
-    for (int i = threadIdx.x; i < n; i += ATT_NT) tab[i] = min(max(src[i], 0), hi);
+    for (int i = threadIdx.x; i < n; i += ATT_NT) {
+      int id = min(max(src[i], 0), hi);
+      if (CELLS && a.cell_pages) {  // the cell's row in the pool less its head's 16 rows: page * hkv * 16 + slot
+        const int64_t pg = min(max((int64_t)a.cell_pages[id >> 4], (int64_t)0), a.cell_npages - 1);
+        id = (int)(pg * a.hkv * 16 + (id & 15));
+      }
+      tab[i] = id;
+    }
     if constexpr (CELLS) {
       const uint8_t* rs = a.real + (int64_t)qcell * a.ctx + 16 * t0;
       for (int i = threadIdx.x; i < 16 * (t1 - t0); i += ATT_NT) flags[i] = i < n ? rs[i] : 0;
@@ -107,7 +118,7 @@ __global__ __launch_bounds__(ATT_NT, 3) void k_attn_split(AttnArgs a) {  // (3 b
   auto row_off = [&](int tile, int tok) -> int64_t {  // elements from the K / V base to a tile position's row
     if constexpr (CELLS) {
       const int i = min((tile - t0) * 16 + tok, a.ctx - 16 * t0 - 1);
-      return ((int64_t)h * a.kv_len + tab[i]) * D;
+      return ((int64_t)h * (a.cell_pages ? 16 : a.kv_len) + tab[i]) * D;
     } else {
       const int64_t phys = tab[tile - t0];
       return ((phys * a.hkv + h) * 16 + tok) * D;
@@ -389,7 +400,13 @@ __global__ __launch_bounds__(ATT_MERGE_NT) void k_attn_merge(AttnArgs a) {
     const int group = a.hq / a.hkv;
     const int h = CELLS ? unit % a.hkv : unit;
     const int qt = CELLS ? unit / a.hkv : row / group, qh = h * group + (CELLS ? row : row % group);
-    ((XT*)a.out)[((int64_t)qt * a.hq + qh) * D + 16 * dt + (t >> 2)] = from_f32<XT>(acc * s_inv[rq]);
+    const int dim = 16 * dt + (t >> 2);
+    XT o = from_f32<XT>(acc * s_inv[rq]);
+    if (a.gate) {  // attention.py:261: out * sigmoid(gate), the sigmoid and the product each rounded to the type
+      const float g = to_f32(((const XT*)a.gate)[qt * a.gate_ts + qh * a.gate_hs + dim]);
+      o = from_f32<XT>(to_f32(o) * to_f32(from_f32<XT>(1.0f / (1.0f + expf(-g)))));
+    }
+    ((XT*)a.out)[((int64_t)qt * a.hq + qh) * D + dim] = o;
   }
 }
 
@@ -498,9 +515,14 @@ size_t sh_paged_attn_workspace(int64_t n_q, int64_t hq, int64_t hkv, int64_t hea
                        (int)head_dim);
 }
 
-int sh_paged_attn(const void* q, const void* k_pages, const void* v_pages, const int32_t* page_table, int64_t n_pages,
-                  int64_t ctx_len, int64_t n_q, int64_t hq, int64_t hkv, int64_t head_dim, float scale, int dtype,
-                  void* out, void* workspace, size_t workspace_bytes, void* stream) {
+}  // extern "C"
+
+namespace {
+
+int paged_attn(const void* q, const void* k_pages, const void* v_pages, const int32_t* page_table, int64_t n_pages,
+               int64_t ctx_len, int64_t n_q, int64_t hq, int64_t hkv, int64_t head_dim, float scale, int dtype,
+               const void* gate, int64_t gate_ts, int64_t gate_hs, void* out, void* workspace, size_t workspace_bytes,
+               void* stream) {
   if (n_q <= 0) return OK;
   if (hkv <= 0 || hq <= 0 || hq % hkv) return fail(E_SHAPE, "paged_attn: %lld query heads over %lld KV heads",
                                                    (long long)hq, (long long)hkv);
@@ -535,6 +557,7 @@ int sh_paged_attn(const void* q, const void* k_pages, const void* v_pages, const
   a.units = (int)hkv;
   a.rows = (int)(n_q * (hq / hkv));
   a.scale_log2 = scale * 1.4426950408889634f;
+  a.gate = gate, a.gate_ts = gate_ts, a.gate_hs = gate_hs;
   attn_ws_carve(&a, (float*)workspace, a.units, a.rows, a.tiles, (a.rows + 63) / 64, (int)head_dim);
   return with_half_dtype(dtype, [&](auto* tp) {
     using XT = std::remove_pointer_t<decltype(tp)>;
@@ -543,15 +566,40 @@ int sh_paged_attn(const void* q, const void* k_pages, const void* v_pages, const
   });
 }
 
+}  // namespace
+
+extern "C" {
+
+int sh_paged_attn(const void* q, const void* k_pages, const void* v_pages, const int32_t* page_table, int64_t n_pages,
+                  int64_t ctx_len, int64_t n_q, int64_t hq, int64_t hkv, int64_t head_dim, float scale, int dtype,
+                  void* out, void* workspace, size_t workspace_bytes, void* stream) {
+  return paged_attn(q, k_pages, v_pages, page_table, n_pages, ctx_len, n_q, hq, hkv, head_dim, scale, dtype, nullptr,
+                    0, 0, out, workspace, workspace_bytes, stream);
+}
+
+int sh_paged_attn_gated(const void* q, const void* k_pages, const void* v_pages, const int32_t* page_table,
+                        int64_t n_pages, int64_t ctx_len, int64_t n_q, int64_t hq, int64_t hkv, int64_t head_dim,
+                        float scale, int dtype, const void* gate, int64_t gate_token_stride, int64_t gate_head_stride,
+                        void* out, void* workspace, size_t workspace_bytes, void* stream) {
+  if (n_q > 0 && !gate) return fail(E_ARG, "paged_attn_gated: null gate");
+  return paged_attn(q, k_pages, v_pages, page_table, n_pages, ctx_len, n_q, hq, hkv, head_dim, scale, dtype, gate,
+                    gate_token_stride, gate_head_stride, out, workspace, workspace_bytes, stream);
+}
+
 size_t sh_cells_attn_workspace(int64_t n_q, int64_t hq, int64_t hkv, int64_t head_dim, int64_t cells) {
   if (n_q <= 0 || hkv <= 0 || hq % hkv || cells <= 0) return 0;
   return attn_ws_carve(nullptr, nullptr, (int)(n_q * hkv), (int)(hq / hkv), (int)((cells + 15) / 16), 1,
                        (int)head_dim);
 }
 
-int sh_cells_attn(const void* q, const void* k, const void* v, int64_t kv_len, const int32_t* cells,
-                  const uint8_t* real, int64_t n_cells, int64_t n_q, int64_t hq, int64_t hkv, int64_t head_dim,
-                  float scale, int dtype, void* out, void* workspace, size_t workspace_bytes, void* stream) {
+}  // extern "C"
+
+namespace {
+
+int cells_attn(const void* q, const void* k, const void* v, int64_t kv_len, const int32_t* cells,
+               const uint8_t* real, int64_t n_cells, int64_t n_q, int64_t hq, int64_t hkv, int64_t head_dim,
+               float scale, int dtype, const int32_t* page_table, int64_t n_pages, const void* gate, int64_t gate_ts,
+               int64_t gate_hs, void* out, void* workspace, size_t workspace_bytes, void* stream) {
   if (n_q <= 0) return OK;
   if (hkv <= 0 || hq <= 0 || hq % hkv) return fail(E_SHAPE, "cells_attn: %lld query heads over %lld KV heads",
                                                    (long long)hq, (long long)hkv);
@@ -586,12 +634,38 @@ int sh_cells_attn(const void* q, const void* k, const void* v, int64_t kv_len, c
   a.units = (int)(n_q * hkv);
   a.rows = (int)(hq / hkv);
   a.scale_log2 = scale * 1.4426950408889634f;
+  a.gate = gate, a.gate_ts = gate_ts, a.gate_hs = gate_hs;
+  a.cell_pages = page_table, a.cell_npages = n_pages;
   attn_ws_carve(&a, (float*)workspace, a.units, a.rows, a.tiles, 1, (int)head_dim);
   return with_half_dtype(dtype, [&](auto* tp) {
     using XT = std::remove_pointer_t<decltype(tp)>;
     return head_dim == 256 ? launch_attn<XT, 256, true>(a, (hipStream_t)stream)
                            : launch_attn<XT, 128, true>(a, (hipStream_t)stream);
   });
+}
+
+}  // namespace
+
+extern "C" {
+
+int sh_cells_attn(const void* q, const void* k, const void* v, int64_t kv_len, const int32_t* cells,
+                  const uint8_t* real, int64_t n_cells, int64_t n_q, int64_t hq, int64_t hkv, int64_t head_dim,
+                  float scale, int dtype, void* out, void* workspace, size_t workspace_bytes, void* stream) {
+  return cells_attn(q, k, v, kv_len, cells, real, n_cells, n_q, hq, hkv, head_dim, scale, dtype, nullptr, 0,
+                    nullptr, 0, 0, out, workspace, workspace_bytes, stream);
+}
+
+int sh_cells_attn_paged(const void* q, const void* k_pages, const void* v_pages, const int32_t* page_table,
+                        int64_t n_pages, const int32_t* cells, const uint8_t* real, int64_t n_cells, int64_t n_q,
+                        int64_t hq, int64_t hkv, int64_t head_dim, float scale, int dtype, const void* gate,
+                        int64_t gate_token_stride, int64_t gate_head_stride, void* out, void* workspace,
+                        size_t workspace_bytes, void* stream) {
+  if (n_q > 0 && (!page_table || n_pages <= 0)) return fail(E_ARG, "cells_attn_paged: no page table");
+  if (n_pages * hkv * 16 * head_dim * 2 > (int64_t)UINT32_MAX)
+    return fail(E_UNSUPPORTED, "cells_attn_paged: a K or V pool of more than 4 GiB");
+  return cells_attn(q, k_pages, v_pages, n_pages * 16, cells, real, n_cells, n_q, hq, hkv, head_dim, scale, dtype,
+                    page_table, n_pages, gate, gate_token_stride, gate_head_stride, out, workspace, workspace_bytes,
+                    stream);
 }
 
 }  // extern "C"

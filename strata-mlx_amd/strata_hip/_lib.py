@@ -58,6 +58,12 @@ PROTOTYPES = {
     "sh_paged_attn_workspace": [c_i64, c_i64, c_i64, c_i64, c_i64],
     "sh_paged_attn": [c_vp, c_vp, c_vp, c_vp, c_i64, c_i64, c_i64, c_i64, c_i64, c_i64, ctypes.c_float, c_int, c_vp,
                       c_vp, c_sz, c_vp],
+    "sh_paged_attn_gated": [c_vp, c_vp, c_vp, c_vp, c_i64, c_i64, c_i64, c_i64, c_i64, c_i64, ctypes.c_float, c_int,
+                            c_vp, c_i64, c_i64, c_vp, c_vp, c_sz, c_vp],
+    "sh_cells_attn_paged": [c_vp, c_vp, c_vp, c_vp, c_i64, c_vp, c_vp, c_i64, c_i64, c_i64, c_i64, c_i64,
+                            ctypes.c_float, c_int, c_vp, c_i64, c_i64, c_vp, c_vp, c_sz, c_vp],
+    "sh_qk_rope": [c_vp, c_int, c_i64, c_i64, c_i64, c_i64, c_vp, ctypes.c_float, c_vp, c_vp, c_i64, c_vp, c_int, c_vp],
+    "sh_kv_append": [c_vp, c_vp, c_i64, c_i64, c_i64, c_int, c_vp, c_vp, c_vp, c_i64, c_i64, c_vp],
     "sh_cells_attn_workspace": [c_i64, c_i64, c_i64, c_i64, c_i64],
     "sh_cells_attn": [c_vp, c_vp, c_vp, c_i64, c_vp, c_vp, c_i64, c_i64, c_i64, c_i64, c_i64, ctypes.c_float, c_int,
                       c_vp, c_vp, c_sz, c_vp],
