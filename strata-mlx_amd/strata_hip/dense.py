@@ -60,6 +60,18 @@ class BlockLinear:
         return out.reshape(*lead, rows)
 
 
+class FloatLinear:
+    """A float16 / bfloat16 weight (rows, cols) called like `nn.Linear`: x @ W^T in x's type (torch.matmul, a plain
+    GEMM on hipBLASLt; sums in float32). What a float tensor of the file becomes (load.py:243-252)."""
+
+    def __init__(self, weight: torch.Tensor):
+        self.weight = weight
+        self.output_dims, self.input_dims = weight.shape
+
+    def __call__(self, x: torch.Tensor) -> torch.Tensor:
+        return x @ self.weight.to(x.dtype).T
+
+
 class BlockEmbedding:
     """An embedding held as the file's blocks; a token's row is unpacked when the token comes
     (strata_mlx/dense.py:231-244)."""
