@@ -34,16 +34,17 @@ for p in (os.path.join(ROOT, "strata-mlx_amd"), ROOT):
 METRIC = "MoE-layer decode µs + effective HBM GB/s (Q2_0, IQ3_S), batch 1-8 tokens"
 E, D, F, K = 512, 2048, 512, 10
 EXPERT_BYTES = 3 * 294_912  # gate + up + down of one Q2_0 expert
+EXPERT_BYTES_IQ3S = 3 * 450_560  # of one IQ3_S expert (512 x 2048 at 110 bytes a 256)
 HBM_PEAK_GBS = 8000.0
 
 
-def layer_bytes(u: int, b: int) -> int:
-    return (u + 1) * EXPERT_BYTES + b * 9_216 + 4_096
+def layer_bytes(u: int, b: int, expert_bytes: int = EXPERT_BYTES) -> int:
+    return (u + 1) * expert_bytes + b * 9_216 + 4_096
 
 
-def front_bytes(u: int, b: int) -> int:
+def front_bytes(u: int, b: int, expert_bytes: int = EXPERT_BYTES) -> int:
     # gate + up blocks of the chosen and the shared experts, logits and x in, swiglu(gate, up) out
-    return (u + 1) * 2 * 294_912 + b * E * 2 + b * D * 2 + (b * K + b) * F * 2
+    return (u + 1) * 2 * expert_bytes // 3 + b * E * 2 + b * D * 2 + (b * K + b) * F * 2
 
 
 def front_traffic():
@@ -126,6 +127,49 @@ def matvec_stream(dev, steps, warmup):
                                  "matrices": n, "single_us": round(us * 1e6, 2), "single_GBps": round(ub / us / 1e9, 1)}
             print(f"# C2 {kind} B={b}: {res[kind][str(b)]}", file=sys.stderr, flush=True)
         del blocks
+        torch.cuda.empty_cache()
+    return res
+
+
+def matvec_sweep(dev, steps, warmup):
+    """C1 and C2's sweep: one 3072 x 2048 matvec a launch over distinct matrices (a stack past the Infinity Cache,
+    graph-captured launches): Q2_0 with float32 activations (x [1, 2048] float32, out float32: the exact path) and
+    every kind with bf16 activations at B = 1 (Q2_0 and IQ3_S by the MFMA stream, the others by the generic
+    kernels). Bytes a call: the matrix's blocks + x + out."""
+    import torch
+
+    from strata_hip import blocks as SB
+    from strata_hip import synth
+
+    R, C = 3072, 2048
+    res = {}
+    cases = [("Q2_0", torch.float32)] + [(k, torch.bfloat16) for k in sorted(SB.BLOCK)]
+    for kind, dt in cases:
+        mat = R * SB.row_bytes(kind, C)
+        n = -(-600_000_000 // mat)
+        blocks = synth.random_blocks_gpu(kind, n * R, C, 9, dev).reshape(n, -1)
+        x = torch.randn(1, C, device=dev).to(dt)
+        SB.window_matvec(blocks[0], kind, R, C, x)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            for m in range(n):
+                SB.window_matvec(blocks[m], kind, R, C, x)
+        for _ in range(warmup):
+            g.replay()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(steps):
+            g.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        sec = e0.elapsed_time(e1) * 1e-3 / (steps * n)
+        nbytes = mat + C * x.element_size() + R * x.element_size()
+        key = f"{kind}_{'fp32' if dt == torch.float32 else 'bf16'}"
+        res[key] = {"us": round(sec * 1e6, 2), "GBps": round(nbytes / sec / 1e9, 1),
+                    "frac": round(nbytes / sec / 1e9 / HBM_PEAK_GBS, 4), "matrices": n}
+        print(f"# C1/C2 sweep {key} B=1: {res[key]}", file=sys.stderr, flush=True)
+        del blocks, g
         torch.cuda.empty_cache()
     return res
 
@@ -238,14 +282,20 @@ def prefill_layer(dev, steps, warmup):
     return res
 
 
-def cpu_baseline(raw, inputs, kind, seconds, check_outputs):
+def cpu_baseline(raw, inputs, kind, seconds, check_outputs, threads=1):
     """The oracle's restatement of the reference's CPU path (dequantize the touched experts, numpy matmul in
-    float32, the reference's routing, SwiGLU and combine roundings), one thread, on the host cores."""
+    float32, the reference's routing, SwiGLU and combine roundings) on the host cores: one thread, or `threads`
+    (the touched experts dequantized and multiplied on a pool of that many threads, each product on one BLAS
+    thread: the parallelism is over experts)."""
+    from concurrent.futures import ThreadPoolExecutor
+
     import numpy as np
     from threadpoolctl import threadpool_limits
 
     from oracle import blocks as OB
     from oracle import route as OR
+
+    pool = ThreadPoolExecutor(threads) if threads > 1 else None
 
     def one_layer(lw, logits, x):
         g, u, d, sg, su, sd, wg = lw
@@ -253,19 +303,24 @@ def cpu_baseline(raw, inputs, kind, seconds, check_outputs):
         w = OR.routing_weights(logits, idx)
         B = x.shape[0]
         ys = np.zeros((B, K, D), np.float32)
-        experts = {}
-        for e in np.unique(idx):
-            experts[int(e)] = [OB.dequantize(m[int(e)], kind, shape, {}) for m, shape in ((g, (F, D)), (u, (F, D)), (d, (D, F)))]
-        for t in range(B):
-            for j in range(K):
-                wg_, wu_, wd_ = experts[int(idx[t, j])]
-                h = OR.swiglu(OR.to_bf16(wg_ @ x[t]), OR.to_bf16(wu_ @ x[t]), "bfloat16")
-                ys[t, j] = OR.to_bf16(wd_ @ h)
+
+        def expert(e):
+            mats = [OB.dequantize(m[int(e)], kind, shape, {}) for m, shape in ((g, (F, D)), (u, (F, D)), (d, (D, F)))]
+            for t, j in zip(*np.nonzero(idx == e)):
+                h = OR.swiglu(OR.to_bf16(mats[0] @ x[t]), OR.to_bf16(mats[1] @ x[t]), "bfloat16")
+                ys[t, j] = OR.to_bf16(mats[2] @ h)
+
+        used = np.unique(idx)
+        if pool is None:
+            for e in used:
+                expert(e)
+        else:
+            list(pool.map(expert, used))
         shw = [OB.dequantize(m[0], kind, shape, {}) for m, shape in ((sg, (F, D)), (su, (F, D)), (sd, (D, F)))]
         s = np.stack([OR.to_bf16(shw[2] @ OR.swiglu(OR.to_bf16(shw[0] @ x[t]), OR.to_bf16(shw[1] @ x[t]), "bfloat16"))
                       for t in range(B)])
         gate = OR.to_bf16(x @ wg)
-        return OR.moe_combine(ys, w, gate, s, "bfloat16"), len(np.unique(idx))
+        return OR.moe_combine(ys, w, gate, s, "bfloat16"), len(used)
 
     host = {}
     total_bytes, total_time, layers_done, checks = 0, 0.0, 0, {}
@@ -291,45 +346,19 @@ def cpu_baseline(raw, inputs, kind, seconds, check_outputs):
             l += 1
             if total_time >= seconds or l >= len(raw):
                 break
+    if pool is not None:
+        pool.shutdown()
     return total_bytes / total_time / 1e9, total_time, layers_done, l, checks
 
 
-def main():
-    ap = argparse.ArgumentParser()
-    ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--layers", type=int, default=48)
-    ap.add_argument("--batches", default="1,2,4,8")
-    ap.add_argument("--kind", default="Q2_0")
-    ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--cpu-seconds", type=float, default=15.0)
-    ap.add_argument("--no-matvec", action="store_true")
-    ap.add_argument("--no-attention", action="store_true")
-    ap.add_argument("--no-prefill", action="store_true")
-    args = ap.parse_args()
-    if args.gpus != 1:
-        print(f"bench.py: --gpus {args.gpus}: this path runs and is measured on one GPU (expert parallelism across "
-              f"GPUs is not implemented); run with --gpus 1", file=sys.stderr)
-        sys.exit(2)
-
+def moe_pass(layers, batches, args, dev, iq3s=False):
+    """One decode pass through the layers at each width, timed as a captured graph; and the front kernel alone."""
     import numpy as np
     import torch
 
-    import strata_hip
     from strata_hip import fused as SF
-    from strata_hip import tables as T
 
-    strata_hip.load()
-    T.use(T.synthetic(0))
-    dev = torch.device("cuda:0")
-    batches = [int(b) for b in args.batches.split(",")]
-    t_setup = time.perf_counter()
-    layers, raw = build_layers(args.layers, dev, args.kind)
-    torch.cuda.synchronize()
-    print(f"# {args.layers} layers of {args.kind} experts on the GPU in {time.perf_counter() - t_setup:.1f} s",
-          file=sys.stderr, flush=True)
-
+    kind_bytes = EXPERT_BYTES_IQ3S if iq3s else EXPERT_BYTES
     per_batch, inputs = {}, {}
     all_bytes, all_time = 0, 0.0
     gu_bytes, gu_time, gu_launches = 0, 0.0, 0
@@ -341,7 +370,7 @@ def main():
         xs = [torch.randn(b, D, device=dev, generator=gen).to(torch.bfloat16) for _ in layers]
         outs = [torch.empty(b, D, device=dev, dtype=torch.bfloat16) for _ in layers]
         uniq = [int(torch.unique(SF.top_k(lg, K)).numel()) for lg in logits]
-        bytes_pass = sum(layer_bytes(u, b) for u in uniq)
+        bytes_pass = sum(layer_bytes(u, b, kind_bytes) for u in uniq)
         stream.wait_stream(torch.cuda.current_stream())  # the inputs were made on the default stream
         with torch.cuda.stream(stream):
             for m, lg, x, o in zip(layers, logits, xs, outs):  # first calls allocate the workspaces
@@ -384,25 +413,85 @@ def main():
                         "front_us": round(gu_ms * 1e3 / n_layers, 3)}
         all_bytes += bytes_pass * args.steps
         all_time += ms * 1e-3
-        gu_bytes += sum(front_bytes(u, b) for u in uniq) * args.steps
+        gu_bytes += sum(front_bytes(u, b, kind_bytes) for u in uniq) * args.steps
         gu_time += gu_ms * 1e-3
         gu_launches += n_layers
         inputs[b] = list(zip(logits, xs, outs))
-        print(f"# B={b}: {per_batch[b]}", file=sys.stderr, flush=True)
+        print(f"# {'IQ3_S' if iq3s else 'Q2_0'} B={b}: {per_batch[b]}", file=sys.stderr, flush=True)
+
+    return per_batch, inputs, all_bytes, all_time, gu_bytes, gu_time, gu_launches
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--layers", type=int, default=48)
+    ap.add_argument("--batches", default="1,2,4,8")
+    ap.add_argument("--kind", default="Q2_0")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=8.0)
+    ap.add_argument("--no-matvec", action="store_true")
+    ap.add_argument("--no-attention", action="store_true")
+    ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--no-iq3s", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: --gpus {args.gpus}: this path runs and is measured on one GPU (expert parallelism across "
+              f"GPUs is not implemented); run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+
+    import numpy as np
+    import torch
+
+    import strata_hip
+    from strata_hip import fused as SF
+    from strata_hip import tables as T
+
+    strata_hip.load()
+    T.use(T.synthetic(0))
+    dev = torch.device("cuda:0")
+    batches = [int(b) for b in args.batches.split(",")]
+    t_setup = time.perf_counter()
+    layers, raw = build_layers(args.layers, dev, args.kind)
+    torch.cuda.synchronize()
+    print(f"# {args.layers} layers of {args.kind} experts on the GPU in {time.perf_counter() - t_setup:.1f} s",
+          file=sys.stderr, flush=True)
+
+    per_batch, inputs, all_bytes, all_time, gu_bytes, gu_time, gu_launches = moe_pass(layers, batches, args, dev)
+    iq3s = None
+    if not args.no_iq3s:  # the metric's second kind: the same pass over IQ3_S experts (not part of `value`)
+        del layers
+        torch.cuda.empty_cache()
+        layers_iq, _ = build_layers(args.layers, dev, "IQ3_S")
+        iq3s, _, b_iq, t_iq, *_ = moe_pass(layers_iq, batches, args, dev, iq3s=True)
+        iq3s = {"per_batch": {str(k): v for k, v in iq3s.items()}, "GBps": round(b_iq / t_iq / 1e9, 1)}
+        del layers_iq
+        torch.cuda.empty_cache()
 
     matvec = None if args.no_matvec else matvec_stream(dev, max(3, args.steps // 4), args.warmup)
+    sweep = None if args.no_matvec else matvec_sweep(dev, max(3, args.steps // 4), args.warmup)
     attention = None if args.no_attention else attention_decode(dev, max(3, args.steps // 4), args.warmup)
     prefill = None if args.no_prefill else prefill_layer(dev, max(3, args.steps // 4), args.warmup)
     value = all_bytes / all_time / 1e9
     achieved = gu_bytes / gu_time / 1e9
     traffic = front_traffic()
-    cpu = None
+    cpu = cpu1 = None
     if not args.no_cpu:
-        gbs, secs, n_done, n_layers_used, checks = cpu_baseline(raw, inputs, args.kind, args.cpu_seconds, True)
-        cpu = {"value": round(gbs, 4), "unit": "GB/s", "cores": 1, "kind": "port",
-               "sample": f"{n_done} layer decodes (layers 0..{n_layers_used - 1} at B = {args.batches}), "
-                         f"{secs:.1f} s: numpy dequantize of the touched experts + float32 matmul, one thread",
-               "check_vs_gpu_rel_err": {str(k): round(v, 6) for k, v in checks.items()}}
+        cores = len(os.sched_getaffinity(0))
+        legs = {}
+        for threads in (1, cores):
+            gbs, secs, n_done, n_layers_used, checks = cpu_baseline(raw, inputs, args.kind, args.cpu_seconds,
+                                                                    threads == 1, threads)
+            legs[threads] = {"value": round(gbs, 4), "unit": "GB/s", "cores": threads, "kind": "port",
+                             "sample": f"{n_done} layer decodes (layers 0..{n_layers_used - 1} at B = {args.batches}), "
+                                       f"{secs:.1f} s: numpy dequantize of the touched experts + float32 matmul, "
+                                       f"{threads} thread(s) over the experts, one BLAS thread each"}
+            if checks:
+                legs[threads]["check_vs_gpu_rel_err"] = {str(k): round(v, 6) for k, v in checks.items()}
+            print(f"# CPU {threads} thread(s): {legs[threads]}", file=sys.stderr, flush=True)
+        cpu, cpu1 = legs[cores], legs[1]
     line = {
         "metric": METRIC, "value": round(value, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(all_time * 1e3 / args.steps, 4), "higher_is_better": True,
@@ -412,6 +501,7 @@ def main():
                    "step": "one decode pass through the layers at each batch width"},
         "per_batch": {str(k): v for k, v in per_batch.items()},
         "matvec_3072x2048": matvec,
+        "matvec_3072x2048_one_a_launch": sweep,
         "paged_attention": attention,
         "prefill_layer": prefill,
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
@@ -419,6 +509,8 @@ def main():
                      "bytes_per_launch": round(gu_bytes / gu_launches), "launches": gu_launches,
                      "us_per_launch": round(gu_time * 1e6 / gu_launches, 3)},
         "cpu_baseline": cpu,
+        "cpu_baseline_1thread": cpu1,
+        "moe_iq3s": iq3s,
     }
     print(json.dumps(line))
 
