@@ -134,11 +134,12 @@ int sh_tiles_of(const int32_t* idx, int64_t pairs, int64_t k, int64_t experts, i
  * (fused.py:491); gate/up/down of each token's experts read straight from the GGUF stacks, SwiGLU with the
  * reference's roundings (strata_mlx/blocks.py:819-829); the shared expert and its gate x . shared_gate_w; the
  * combine (fused.py:448-481). No host synchronisation: for 512 experts, d_model 2048, d_ff 512 (16-byte aligned
- * operands) two kernels (route + gate/up + SwiGLU; down + combine), otherwise three (route; gate/up; down +
- * combine). kind / kind_down: Q2_0 or IQ3_S; dtype: F16 or BF16; d_model, d_ff multiples of 256; experts a multiple
- * of 64 up to 2048. idx_out (tokens x k int32) and w_out (tokens x k float32) are optional copies of the choice.
- * workspace: sh_moe_workspace() bytes; nothing in it has to start at zero (each call clears what it counts in);
- * calls sharing a workspace must not overlap. */
+ * operands) two kernels (route + gate/up + SwiGLU, then down + combine), otherwise three (route; gate/up; down +
+ * combine). kind / kind_down: Q2_0 or IQ3_S; dtype: F16 or BF16;
+ * d_model, d_ff multiples of 256; experts a multiple of 64 up to 2048. idx_out (tokens x k int32) and w_out
+ * (tokens x k float32) are optional copies of the choice. workspace: sh_moe_workspace() bytes, zeroed once before
+ * its first call (the launch's counters, at its head whatever the shape, must start at zero; every call leaves them
+ * at zero, so one workspace serves calls of any shape in turn); calls sharing a workspace must not overlap. */
 size_t sh_moe_workspace(int64_t tokens, int64_t k, int64_t d_model, int64_t d_ff, int dtype);
 int sh_moe_decode(int kind, int kind_down, const void* gate, const void* up, const void* down, int64_t experts,
                   const void* shared_gate, const void* shared_up, const void* shared_down, const void* shared_gate_w,
@@ -148,7 +149,8 @@ int sh_moe_decode(int kind, int kind_down, const void* gate, const void* up, con
 /* No counterpart in the reference: sh_moe_decode for callers that cannot allocate (code under HIP graph capture,
  * tight serving loops, harnesses that forbid hipMalloc). The same arguments without the workspace: the library's
  * own device array of sh_moe_scratch_bytes() (8 MiB) on each GPU serves as it, found once per device at the first
- * call there. Nothing is allocated. Shapes whose workspace (sh_moe_workspace) exceeds the array are refused with
+ * call there (that first call also clears the array's counters on `stream`). Nothing is allocated. Shapes whose
+ * workspace (sh_moe_workspace) exceeds the array are refused with
  * SH_E_WORKSPACE before anything is launched. Every call on a GPU shares that GPU's array: calls that overlap on one
  * GPU (two streams, two threads) race and must be ordered by the caller. */
 size_t sh_moe_scratch_bytes(void);
@@ -162,6 +164,11 @@ int sh_moe_decode_noalloc(int kind, int kind_down, const void* gate, const void*
  * after it (default 4). Both give the same bits. Returns the previous bound. Process-wide; not for use while
  * another thread launches sh_moe_decode. */
 int sh_moe_set_tail_combine(int upto);
+/* No counterpart in the reference: whether sh_moe_decode runs the common shape's step (512 experts, d_model 2048,
+ * d_ff 512) as one launch (gate / up and down blocks in one grid) instead of two. The one-launch form is switched
+ * off: on = 1 is refused with SH_E_UNSUPPORTED (it made an illegal memory access at 2 tokens whose cause is not
+ * found); on = 0 returns the previous setting (0). */
+int sh_moe_set_one_launch(int on);
 /* One of sh_moe_decode's kernels alone (phase 0 route, 1 gate/up, 2 down + combine; for the two-kernel shape
  * phases 0 and 1 are both the route + gate/up kernel), in that order over one workspace: what a caller times or
  * interleaves kernel by kernel. */

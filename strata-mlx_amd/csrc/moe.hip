@@ -17,6 +17,7 @@
 // order its MFMA fragments take them, and are read straight from memory (L2). Grids are sized by the most groups
 // there could be (B*k + 1); blocks past the groups the route found leave at once, so nothing waits on the host.
 #include <atomic>
+#include <cassert>
 #include <mutex>
 
 #include "launch.h"
@@ -35,7 +36,9 @@ inline bool vpl_bad(int64_t experts) {
   return experts % 64 || v < 1 || v > 32 || (v & (v - 1));
 }
 
-// the workspace, carved from one caller buffer
+// the workspace, carved from one caller buffer: the control words first, at the same offsets whatever the shape
+// (the one-launch layer needs them at zero when it starts, and its last block leaves them at zero, so a workspace
+// used for several shapes in turn keeps them), then the shape's arrays
 struct MoeWs {
   int32_t* n_groups;  // [1]
   int32_t* g_expert;  // [G]: expert, or `experts` for the shared expert
@@ -47,10 +50,26 @@ struct MoeWs {
   uint8_t* xp;        // [B][D]: the hidden states staged for gate/up's kind (xmv.h stage_index)
   uint8_t* h;         // [B*k + B][F]: swiglu(gate, up), staged for down's kind (natural order in the two-kernel path)
   float* y;           // [B*k + B][D]: each pair's down outputs, rounded to the activation type (the common shape)
+  // counters, each in a 256-byte line of its own (CTR_STRIDE words apart): agent-scope atomics on one line are
+  // done one after another, about 10 ns each, so hundreds of blocks counting on one line would wait microseconds.
+  // The one-launch layer's come in two sets, used by calls in turn: `par` names the set a call uses, and the call's
+  // last block to draw a ticket clears the other set for the next call and switches `par` to it.
   int32_t* cnt;       // [D / 64]: the tail's finished items a row tile when it combines, zero between calls
+  int32_t* par;       // [1]: one-launch layer: the set of counters the next call uses (0 or 1)
+  int32_t* ticket;    // [1]: one-launch layer: tickets drawn, zero between calls
+  int32_t* gdone;     // [2][G]: one-launch layer: gate / up items done a group
+  int32_t* gall;      // [2]: one-launch layer: groups complete
+  int32_t* gflag;     // [2][8]: one-launch layer: every group complete (eight copies: the down blocks poll by eighths)
+  int32_t* err;       // [1]: set (and left set) if a wait gave up or the counters were not at zero
 };
+constexpr int MOE_CNT_WORDS = MOE_MAX_D / 64 + 1;
+constexpr int CTR_STRIDE = 64;
 
-static inline size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
+constexpr size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
+// the control words' bytes at the head of every workspace
+constexpr size_t MOE_HEAD_BYTES = align256(4 * CTR_STRIDE * MOE_CNT_WORDS) + 2 * 256 +
+                                  align256(4 * CTR_STRIDE * 2 * (MOE_MAX_PAIRS + 1)) + align256(4 * CTR_STRIDE * 2) +
+                                  align256(4 * CTR_STRIDE * 2 * 8) + 256;
 
 static size_t moe_carve(MoeWs* ws, uint8_t* base, int64_t B, int64_t k, int64_t D, int64_t F, int es) {
   const int64_t G = B * k + 1, P = B * k + B;
@@ -61,6 +80,14 @@ static size_t moe_carve(MoeWs* ws, uint8_t* base, int64_t B, int64_t k, int64_t 
     return p;
   };
   MoeWs w;
+  w.cnt = (int32_t*)take((size_t)4 * CTR_STRIDE * MOE_CNT_WORDS);
+  w.par = (int32_t*)take(4);
+  w.ticket = (int32_t*)take(4);
+  w.gdone = (int32_t*)take((size_t)4 * CTR_STRIDE * 2 * (MOE_MAX_PAIRS + 1));
+  w.gall = (int32_t*)take((size_t)4 * CTR_STRIDE * 2);
+  w.gflag = (int32_t*)take((size_t)4 * CTR_STRIDE * 2 * 8);
+  w.err = (int32_t*)take(4);
+  assert(off == MOE_HEAD_BYTES);
   w.n_groups = (int32_t*)take(4);
   w.g_expert = (int32_t*)take(4 * G);
   w.g_ntok = (int32_t*)take(4 * G);
@@ -71,7 +98,6 @@ static size_t moe_carve(MoeWs* ws, uint8_t* base, int64_t B, int64_t k, int64_t 
   w.xp = take((size_t)B * D * es);
   w.h = take((size_t)P * F * es);
   w.y = (float*)take((size_t)P * D * 4);
-  w.cnt = (int32_t*)take((size_t)4 * (D / 64 + 1));
   if (ws) *ws = w;
   return off;
 }
@@ -409,6 +435,10 @@ constexpr int FRONT_WAVES = 8;
 constexpr int TAIL_COMBINE_UPTO = 4;  // tokens up to which the tail combines in-kernel
 // the same bound as set at run time (sh_moe_set_tail_combine): 0 sends every window to the combine kernel
 static std::atomic<int> g_tail_combine_upto{TAIL_COMBINE_UPTO};
+// whether the common shape's step runs as one launch (sh_moe_set_one_launch). Off, and it cannot be switched on:
+// the one-launch layer (k_moe_layer) made an illegal memory access at 2 tokens (Q2_0, float16) whose cause is not
+// found; until it is, every window takes the two launches.
+static std::atomic<int> g_one_launch{0};
 
 // the pairs of group expert e in token order, into this wave's wp[0, n): pair t * K + j of each token t choosing e
 // (a token chooses an expert at most once), or every token's shared pair P + t for the shared expert (e == E)
@@ -436,14 +466,15 @@ __device__ __forceinline__ int group_pairs(int e, int E, const int* s_idx, int B
   return n;
 }
 
-// a block's run of items: chunk c of group g's TILES items, chunks of `per` items, per the least that leaves a
-// block for every chunk (the grid holds at least one block a group). Returns false for a block past the chunks.
-template <int TILES> __device__ __forceinline__ bool group_chunk(int groups, int& g, int& first, int& last) {
-  int per = max(1, (groups * TILES + (int)gridDim.x - 1) / (int)gridDim.x);
-  while (per < TILES && groups * ((TILES + per - 1) / per) > (int)gridDim.x) ++per;
+// block `bid` of `nblk`'s run of items: chunk c of group g's TILES items, chunks of `per` items, per the least that
+// leaves a block for every chunk (at least one block a group). Returns false for a block past the chunks.
+template <int TILES>
+__device__ __forceinline__ bool group_chunk(int groups, int nblk, int bid, int& g, int& first, int& last) {
+  int per = max(1, (groups * TILES + nblk - 1) / nblk);
+  while (per < TILES && groups * ((TILES + per - 1) / per) > nblk) ++per;
   const int cpg = (TILES + per - 1) / per;
-  g = blockIdx.x / cpg;
-  const int c = blockIdx.x - g * cpg;
+  g = bid / cpg;
+  const int c = bid - g * cpg;
   first = g * TILES + c * per;
   last = g * TILES + min(TILES, (c + 1) * per);
   return g < groups;
@@ -467,47 +498,37 @@ struct FrontPlan {
   int red_off;   // [2][2][7][64][TPG] floats: gate's and up's partial sums of waves 1..7, the last two items
 };
 
-template <int KIND, typename XT, typename LT, int TPG>
-__global__ __launch_bounds__(FRONT_WAVES * 64) void k_moe_front(
-    const uint8_t* __restrict__ gate, const uint8_t* __restrict__ up, const uint8_t* __restrict__ sh_gate,
-    const uint8_t* __restrict__ sh_up, const LT* __restrict__ logits, const XT* __restrict__ x,
-    const XT* __restrict__ wgt, int K, int B, FrontPlan fp, const uint8_t* __restrict__ signed_tab, MoeWs ws) {
-  using MT = XT;
+// ---- the route of a window, in every block that needs it
+
+// the route's LDS: the chosen experts and weights of every pair, the flags of the chosen experts, selection scratch
+template <typename LT> struct RouteLds {
+  using key_t = typename RouteKey<LT>::type;
+  int idx[MOE_MAX_PAIRS];
+  float wt[MOE_MAX_PAIRS];
+  uint32_t flag[FRONT_E / 32];
+  key_t tk[FRONT_WAVES][2][16];
+  key_t cand[FRONT_WAVES][64];
+  float ev[FRONT_WAVES][16];
+};
+
+// the groups after the route, as every wave holds them: lane l's flag word (experts 32l .. 32l + 31) and the
+// inclusive count of chosen experts up to it; `total` chosen experts, `groups` = total + 1 (the shared expert last)
+struct RouteGroups {
+  uint32_t word;
+  int incl, total, groups;
+};
+
+// 1. each token's top-k of the logits and the softmax of the chosen (a wave a token, its logits loaded first); the
+// chosen experts flagged as they are found. 2. the groups: the chosen experts in ascending order, then the shared
+// expert, counted by each wave from the flags. Ends past a block barrier.
+template <typename LT>
+__device__ __forceinline__ RouteGroups moe_route(const LT* __restrict__ logits, int K, int B, RouteLds<LT>& r) {
   using RK = RouteKey<LT>;
   using key_t = typename RK::type;
-  constexpr int E = FRONT_E, D = FRONT_D, F = FRONT_F, VPL = E / 64, WORDS = E / 32, TILES = F / 16;
-  constexpr int NT = FRONT_WAVES * 64;
-  constexpr int GPER = KIND == Q2_0 ? D / 64 / FRONT_WAVES : D / 32 / FRONT_WAVES;  // a wave's eighth of the groups
-  using IT = FrontItem<KIND>;
-  constexpr int RB = IT::RB;
-  extern __shared__ u32x4 dyn[];
-  uint8_t* lds = (uint8_t*)dyn;
-  const uint32_t lds_base = SH_LDS_ADDR(dyn);
-  float* red = (float*)(lds + fp.red_off);
+  constexpr int E = FRONT_E, VPL = E / 64, WORDS = E / 32;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int kq = wave;
-  const int P = B * K;
-  __shared__ int s_idx[MOE_MAX_PAIRS];
-  __shared__ float s_wt[MOE_MAX_PAIRS];
-  __shared__ uint32_t s_flag[WORDS];
-  __shared__ int s_wp[FRONT_WAVES][16];
-  __shared__ key_t s_tk[FRONT_WAVES][2][16];
-  __shared__ key_t s_cand[FRONT_WAVES][64];
-  __shared__ float s_ev[FRONT_WAVES][16];
-
-  // the IQ3_S table first: it does not wait on the choice (2048 chunks, four a thread)
-  if constexpr (KIND == IQ3_S) {
-#pragma unroll
-    for (int i = 0; i < IQ3S_SIGNED_BYTES / 16 / NT; ++i) {
-      const int c0 = wave * 64 + i * NT;
-      lds_dma16(signed_tab, 16 * (c0 + lane), lds_base + 16 * c0);
-    }
-  }
-  if (tid < WORDS) s_flag[tid] = 0u;
-
-  // 1. each token's top-k of the logits and the softmax of the chosen (a wave a token, its logits loaded first);
-  // the chosen experts flagged as they are found
+  if (tid < WORDS) r.flag[tid] = 0u;
   {
     key_t key[2][VPL];
 #pragma unroll
@@ -523,76 +544,118 @@ __global__ __launch_bounds__(FRONT_WAVES * 64) void k_moe_front(
     for (int u = 0; u < 2; ++u) {
       const int t = wave + FRONT_WAVES * u;
       if (t >= B) break;
-      wave_top_k<RK, VPL>(key[u], K, s_cand[wave], s_tk[wave][0], s_tk[wave][1]);
+      wave_top_k<RK, VPL>(key[u], K, r.cand[wave], r.tk[wave][0], r.tk[wave][1]);
       // the softmax of the chosen in rank order, as the reference sums it
-      const key_t* sorted = s_tk[wave][1];
+      const key_t* sorted = r.tk[wave][1];
       const float top = RK::value(sorted[0]);
-      if (lane < K) s_ev[wave][lane] = expf(RK::value(sorted[lane]) - top);
+      if (lane < K) r.ev[wave][lane] = expf(RK::value(sorted[lane]) - top);
       __builtin_amdgcn_wave_barrier();
       float sum = 0.0f;
-      for (int r = 0; r < K; ++r) sum += s_ev[wave][r];
+      for (int q = 0; q < K; ++q) sum += r.ev[wave][q];
       if (lane < K) {
         const int e = RK::index(sorted[lane]);
-        s_idx[t * K + lane] = e;
-        s_wt[t * K + lane] = s_ev[wave][lane] / sum;
-        atomicOr(&s_flag[e >> 5], 1u << (e & 31));
+        r.idx[t * K + lane] = e;
+        r.wt[t * K + lane] = r.ev[wave][lane] / sum;
+        atomicOr(&r.flag[e >> 5], 1u << (e & 31));
       }
       __builtin_amdgcn_wave_barrier();
     }
   }
   __syncthreads();
-  // 2. the groups: the chosen experts in ascending order, then the shared expert. Each wave counts them from the
-  // flags itself and finds its block's group (no barrier); block 0 writes every group's expert for the tail.
-  const uint32_t word = lane < WORDS ? s_flag[lane] : 0u;
-  const int cnt = __popc(word);
+  RouteGroups g;
+  g.word = lane < WORDS ? r.flag[lane] : 0u;
+  const int cnt = __popc(g.word);
   int incl = cnt;
 #pragma unroll
   for (int o = 1; o < WORDS; o <<= 1) {
     const int v = __shfl_up(incl, o);
     if (lane >= o) incl += v;
   }
-  const int total = __shfl(incl, WORDS - 1);
-  const int groups = total + 1;
-  if (blockIdx.x == 0) {  // the choice, its weights and the groups' experts for the tail and the caller
-    if (tid < P) {
-      ws.idx[tid] = s_idx[tid];
-      ws.w[tid] = s_wt[tid];
-    }
-    if (wave == 0) {
-      int pos = incl - cnt;
-      for (uint32_t w = word; w; w &= w - 1u) ws.g_expert[pos++] = lane * 32 + __ffs(w) - 1;
-      if (lane == 0) ws.g_expert[total] = E;
-    }
-    if (tid < D / 64) ws.cnt[tid] = 0;  // the tail's row-tile counters
-    if (tid == 0) *ws.n_groups = groups;
-  }
-  if (blockIdx.x == 1 % gridDim.x) {  // the shared expert's gate logit of each token, rounded to the activation type
-    for (int t = wave; t < B; t += FRONT_WAVES) {
-      float acc = 0.0f;
-#pragma unroll
-      for (int j = 0; j < D / 512; ++j) {
-        const u32x4 xv = *(const u32x4*)(x + (int64_t)t * D + 8 * (lane + 64 * j));
-        const u32x4 wv = *(const u32x4*)(wgt + 8 * (lane + 64 * j));
-        const XT* a = (const XT*)&xv;
-        const XT* b = (const XT*)&wv;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) acc = fmaf(to_f32(a[i]), to_f32(b[i]), acc);
-      }
-      acc = wave_sum(acc);
-      if (lane == 0) ws.gsh[t] = to_f32(from_f32<XT>(acc));
-    }
-  }
+  g.incl = incl;
+  g.total = __shfl(incl, WORDS - 1);
+  g.groups = g.total + 1;
+  return g;
+}
 
-  // 3. this block's run of the items: part of one group's
-  int g0, first, last;
-  if (!group_chunk<TILES>(groups, g0, first, last)) return;  // block-uniform
-  int e0 = E;  // the group's expert: the (g0 - excl)-th flag of the word holding it
-  if (g0 < total) {
-    const int at = __builtin_amdgcn_readfirstlane(__ffsll((unsigned long long)__ballot(lane < WORDS && incl > g0)) - 1);
-    uint32_t w = __builtin_amdgcn_readfirstlane((uint32_t)__shfl((int)word, at));
-    for (int k = g0 - (__shfl(incl, at) - __popc(w)); k > 0; --k) w &= w - 1u;
-    e0 = at * 32 + __ffs(w) - 1;
+// the expert of group g (wave-uniform): the (g - before)-th flag of the word holding it; E for the shared group
+__device__ __forceinline__ int group_expert(const RouteGroups& rg, int g) {
+  constexpr int WORDS = FRONT_E / 32;
+  const int lane = threadIdx.x & 63;
+  if (g >= rg.total) return FRONT_E;
+  const int at = __builtin_amdgcn_readfirstlane(__ffsll((unsigned long long)__ballot(lane < WORDS && rg.incl > g)) - 1);
+  uint32_t w = __builtin_amdgcn_readfirstlane((uint32_t)__shfl((int)rg.word, at));
+  for (int k = g - (__shfl(rg.incl, at) - __popc(w)); k > 0; --k) w &= w - 1u;
+  return at * 32 + __ffs(w) - 1;
+}
+
+// the route's results for the caller and the combine kernel (one block writes them): the choice, its weights, the
+// groups' experts, the group count; and clears the down's row-tile counters (two-kernel form)
+template <typename LT>
+__device__ __forceinline__ void route_publish(const RouteGroups& rg, const RouteLds<LT>& r, int P, MoeWs ws,
+                                              bool clear_counters) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  if (tid < P) {
+    ws.idx[tid] = r.idx[tid];
+    ws.w[tid] = r.wt[tid];
   }
+  if (wave == 0) {
+    int pos = rg.incl - __popc(rg.word);
+    for (uint32_t w = rg.word; w; w &= w - 1u) ws.g_expert[pos++] = lane * 32 + __ffs(w) - 1;
+    if (lane == 0) ws.g_expert[rg.total] = FRONT_E;
+  }
+  if (clear_counters && tid < FRONT_D / 64) ws.cnt[tid * CTR_STRIDE] = 0;  // the tail's row-tile counters
+  if (tid == 0) *ws.n_groups = rg.groups;
+}
+
+// the shared expert's gate logit of each token, rounded to the activation type, into gsh (a wave a token)
+template <typename XT>
+__device__ __forceinline__ void shared_gate_logits(const XT* __restrict__ x, const XT* __restrict__ wgt, int B,
+                                                   float* gsh) {
+  constexpr int D = FRONT_D;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  for (int t = wave; t < B; t += FRONT_WAVES) {
+    float acc = 0.0f;
+#pragma unroll
+    for (int j = 0; j < D / 512; ++j) {
+      const u32x4 xv = *(const u32x4*)(x + (int64_t)t * D + 8 * (lane + 64 * j));
+      const u32x4 wv = *(const u32x4*)(wgt + 8 * (lane + 64 * j));
+      const XT* a = (const XT*)&xv;
+      const XT* b = (const XT*)&wv;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) acc = fmaf(to_f32(a[i]), to_f32(b[i]), acc);
+    }
+    acc = wave_sum(acc);
+    if (lane == 0) gsh[t] = to_f32(from_f32<XT>(acc));
+  }
+}
+
+// ---- gate / up items of a block's run: part of one group's 16-row items. `signal` (one-launch layer): 0, or one
+// more than the counter set to count the block's items into when its rows of h are out.
+
+template <int KIND, typename XT, typename LT, int TPG>
+__device__ __forceinline__ void front_items(int bid, int nblk, const RouteGroups& rg, const RouteLds<LT>& r,
+                                            const uint8_t* __restrict__ gate, const uint8_t* __restrict__ up,
+                                            const uint8_t* __restrict__ sh_gate, const uint8_t* __restrict__ sh_up,
+                                            const XT* __restrict__ x, int K, int B, const FrontPlan& fp, MoeWs ws,
+                                            int signal, int (*s_wp)[16]) {
+  using MT = XT;
+  constexpr int E = FRONT_E, D = FRONT_D, F = FRONT_F, TILES = F / 16;
+  constexpr int NT = FRONT_WAVES * 64;
+  constexpr int GPER = KIND == Q2_0 ? D / 64 / FRONT_WAVES : D / 32 / FRONT_WAVES;  // a wave's eighth of the groups
+  using IT = FrontItem<KIND>;
+  constexpr int RB = IT::RB;
+  extern __shared__ u32x4 dyn[];
+  uint8_t* lds = (uint8_t*)dyn;
+  const uint32_t lds_base = SH_LDS_ADDR(dyn);
+  float* red = (float*)(lds + fp.red_off);
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int kq = wave;
+  const int P = B * K;
+
+  int g0, first, last;
+  if (!group_chunk<TILES>(rg.groups, nblk, bid, g0, first, last)) return;  // block-uniform
+  const int e0 = group_expert(rg, g0);
 
   // this thread's chunks of an item: matrix (0 gate, 1 up) and byte offset from the item's first row; the slot's
   // tail past the two matrices re-reads up's last chunk. Each wave waits on its own count of loads.
@@ -611,16 +674,16 @@ __global__ __launch_bounds__(FRONT_WAVES * 64) void k_moe_front(
   const uint8_t* gate_e = e0 == E ? sh_gate : gate + (int64_t)e0 * ebytes;
   const uint8_t* up_e = e0 == E ? sh_up : up + (int64_t)e0 * ebytes;
   auto issue = [&](int item) {
-    const int r = item - g0 * TILES;
-    const uint8_t* gs = gate_e + (int64_t)r * 16 * RB;
-    const uint8_t* us = up_e + (int64_t)r * 16 * RB;
+    const int rr = item - g0 * TILES;
+    const uint8_t* gs = gate_e + (int64_t)rr * 16 * RB;
+    const uint8_t* us = up_e + (int64_t)rr * 16 * RB;
     const uint32_t buf = lds_base + fp.ring_off + (item % fp.nbuf) * IT::SLOT + wave * 1024;
 #pragma unroll
     for (int j = 0; j < IT::LOADS; ++j)
       if (j < loads) lds_dma16p((pre_up[j] ? us : gs) + pre_off[j], buf + j * (NT * 16));
   };
   // the group's tokens and their activation loads, then the ring's first items: both in flight at once
-  const int n_tok = group_pairs(e0, E, s_idx, B, K, s_wp[wave]);
+  const int n_tok = group_pairs(e0, E, r.idx, B, K, s_wp[wave]);
   XRaw<KIND, GPER> xraw;
   {
     int mt = lane_token<TPG>();
@@ -653,8 +716,13 @@ __global__ __launch_bounds__(FRONT_WAVES * 64) void k_moe_front(
           us += rd[RED + w * 64 * TPG + t];
         }
         const int tt = q * TPG + t;
-        if (tt < n_tok)
-          ((XT*)ws.h)[(int64_t)s_wp[0][tt] * F + hrow] = swiglu_one(from_f32<XT>(gs), from_f32<XT>(us));
+        if (tt >= n_tok) continue;
+        XT* at = (XT*)ws.h + (int64_t)s_wp[0][tt] * F + hrow;
+        const XT hv = swiglu_one(from_f32<XT>(gs), from_f32<XT>(us));
+        if (signal)
+          st_agent<XT>(at, hv);
+        else
+          *at = hv;
       }
     }
   };
@@ -664,7 +732,7 @@ __global__ __launch_bounds__(FRONT_WAVES * 64) void k_moe_front(
     lds_sync();  // this item is in LDS for every wave; every wave is done with the item before
     finish();
     if (item + fp.nbuf - 1 < last) issue(item + fp.nbuf - 1);
-    const int r = item - g0 * TILES;
+    const int rr = item - g0 * TILES;
     float acc_g[TPG], acc_u[TPG];
 #pragma unroll
     for (int t = 0; t < TPG; ++t) acc_g[t] = acc_u[t] = 0.0f;
@@ -686,11 +754,53 @@ __global__ __launch_bounds__(FRONT_WAVES * 64) void k_moe_front(
         pg[t] = acc_g[t];
         pu[t] = acc_u[t];
       }
-      hrow = r * 16 + (lane & 15);
+      hrow = rr * 16 + (lane & 15);
     }
   }
   lds_sync();
   finish();
+  if (signal && wave == 0) {
+    // this run's rows of h (wave 0's agent-scope stores) are complete: counted into the group's; the block that
+    // completes a group counts the group, and the one that completes the last group raises the flags
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    if (lane == 0) {
+      const int set = signal - 1, n = last - first;
+      if (__hip_atomic_fetch_add(&ws.gdone[(set * (MOE_MAX_PAIRS + 1) + g0) * CTR_STRIDE], n, __ATOMIC_RELAXED,
+                                 __HIP_MEMORY_SCOPE_AGENT) + n == TILES &&
+          __hip_atomic_fetch_add(&ws.gall[set * CTR_STRIDE], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+              rg.groups - 1) {
+        for (int c = 0; c < 8; ++c)
+          __hip_atomic_store(&ws.gflag[(set * 8 + c) * CTR_STRIDE], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+    }
+  }
+}
+
+template <int KIND, typename XT, typename LT, int TPG>
+__global__ __launch_bounds__(FRONT_WAVES * 64) void k_moe_front(
+    const uint8_t* __restrict__ gate, const uint8_t* __restrict__ up, const uint8_t* __restrict__ sh_gate,
+    const uint8_t* __restrict__ sh_up, const LT* __restrict__ logits, const XT* __restrict__ x,
+    const XT* __restrict__ wgt, int K, int B, FrontPlan fp, const uint8_t* __restrict__ signed_tab, MoeWs ws) {
+  constexpr int NT = FRONT_WAVES * 64;
+  __shared__ RouteLds<LT> r;
+  __shared__ int s_wp[FRONT_WAVES][16];
+  extern __shared__ u32x4 dyn[];
+  const uint32_t lds_base = SH_LDS_ADDR(dyn);
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  // the IQ3_S table first: it does not wait on the choice (2048 chunks, four a thread)
+  if constexpr (KIND == IQ3_S) {
+#pragma unroll
+    for (int i = 0; i < IQ3S_SIGNED_BYTES / 16 / NT; ++i) {
+      const int c0 = wave * 64 + i * NT;
+      lds_dma16(signed_tab, 16 * (c0 + lane), lds_base + 16 * c0);
+    }
+  }
+  const RouteGroups rg = moe_route<LT>(logits, K, B, r);
+  if (blockIdx.x == 0) route_publish<LT>(rg, r, B * K, ws, true);
+  if (blockIdx.x == 1 % gridDim.x) shared_gate_logits<XT>(x, wgt, B, ws.gsh);
+  front_items<KIND, XT, LT, TPG>(blockIdx.x, gridDim.x, rg, r, gate, up, sh_gate, sh_up, x, K, B, fp, ws, 0,
+                                 s_wp);
 }
 
 // the combine (strata_mlx/fused.py:448-462) of output (token t, row): experts in 8 rows j taking k = j, j + 8, ...,
@@ -747,11 +857,19 @@ struct TailPlan {
   int red_off;   // [2][4][64][TPG] floats: the second column half's sums of the last two items
 };
 
-template <int KIND, typename XT, int TPG>
-__global__ __launch_bounds__(FRONT_WAVES * 64) void k_moe_tail(const uint8_t* __restrict__ down,
-                                                               const uint8_t* __restrict__ sh_down, int K, int B,
-                                                               TailPlan tp, const uint8_t* __restrict__ signed_tab,
-                                                               MoeWs ws, int combine, XT* __restrict__ out) {
+// Spins a block may make on a count another block raises before it gives up and flags the workspace (a guard
+// against a hang, never reached when every block runs: the counts it waits on are raised by blocks that wait on
+// nothing)
+constexpr int MOE_MAX_SPINS = 1 << 20;
+
+// ---- down items of a block's run: part of one group's 64-row items, each pair's outputs rounded to the activation
+// type; with `combine`, the block completing a row tile's count combines the tile. `gexp(g)` is group g's expert;
+// w(p) the routing weight of pair p, gsh[t] token t's shared gate logit.
+template <int KIND, typename XT, int TPG, typename GE, typename WF>
+__device__ __forceinline__ void tail_items(int bid, int nblk, int groups, const int* s_idx, GE&& gexp, WF&& wsrc,
+                                           const float* gsh, const uint8_t* __restrict__ down,
+                                           const uint8_t* __restrict__ sh_down, int K, int B, const TailPlan& tp,
+                                           MoeWs ws, int combine, XT* __restrict__ out, int (*s_wp)[16]) {
 #pragma clang fp contract(off)
   using MT = XT;
   using IT = TailItem<KIND>;
@@ -762,39 +880,22 @@ __global__ __launch_bounds__(FRONT_WAVES * 64) void k_moe_tail(const uint8_t* __
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int rg = wave & 3, kh = wave >> 2;
   const int wcol = KIND == Q2_0 ? kh * GPER * 18 : kh * 110;
-  const int P = B * K;
-  __shared__ int s_groups, s_ncomb;
-  __shared__ int s_idx[MOE_MAX_PAIRS], s_gexp[MOE_MAX_PAIRS + 1], s_comb[MOE_MAX_PAIRS + 1];
-  __shared__ int s_wp[FRONT_WAVES][16];
+  __shared__ int s_ncomb;
+  __shared__ int s_comb[TILES];  // the row tiles this block completes (its run's items are distinct tiles)
   extern __shared__ u32x4 dyn[];
   uint8_t* lds = (uint8_t*)dyn;
   const uint32_t lds_base = SH_LDS_ADDR(dyn);
   float* red = (float*)(lds + tp.red_off);
 
-  // the IQ3_S table (it waits on nothing), then the front's choice and groups in one trip
-  if constexpr (KIND == IQ3_S) {
-#pragma unroll
-    for (int i = 0; i < IQ3S_SIGNED_BYTES / 16 / NT; ++i) {
-      const int c0 = wave * 64 + i * NT;
-      lds_dma16(signed_tab, 16 * (c0 + lane), lds_base + 16 * c0);
-    }
-  }
-  if (tid == 0) {
-    s_groups = *ws.n_groups;
-    s_ncomb = 0;
-  }
-  if (tid < P) s_idx[tid] = ws.idx[tid];
-  if (tid <= P) s_gexp[tid] = ws.g_expert[tid];  // entries past the groups are never read
-  __syncthreads();
-  const int groups = s_groups;
   int g0, first, last;  // this block's run of items: part of one group's
-  if (!group_chunk<TILES>(groups, g0, first, last)) return;  // block-uniform; the barrier above waited for the table
+  if (!group_chunk<TILES>(groups, nblk, bid, g0, first, last)) return;  // block-uniform
+  if (tid == 0) s_ncomb = 0;
 
   const int loads = (IT::RUNS - wave + FRONT_WAVES - 1) / FRONT_WAVES;
   int pre_off[IT::LOADS];
 #pragma unroll
   for (int j = 0; j < IT::LOADS; ++j) pre_off[j] = 16 * min((j * FRONT_WAVES + wave) * 64 + lane, IT::CHUNKS - 1);
-  const int e0 = s_gexp[g0];
+  const int e0 = gexp(g0);
   const uint8_t* down_e = e0 == E ? sh_down : down + (int64_t)e0 * D * RB;
   auto issue = [&](int item) {
     const uint8_t* src = down_e + (int64_t)(item - g0 * TILES) * IT::ROWS * RB;
@@ -803,23 +904,22 @@ __global__ __launch_bounds__(FRONT_WAVES * 64) void k_moe_tail(const uint8_t* __
     for (int j = 0; j < IT::LOADS; ++j)
       if (j < loads) lds_dma16(src, pre_off[j], buf + j * (NT * 16));
   };
-  // the group's tokens and their loads of h, then the ring's first items: both in flight at once
   const int n_tok = group_pairs(e0, E, s_idx, B, K, s_wp[wave]);
   XRaw<KIND, GPER> xraw;
   {
+    // the group's tokens and their loads of h, then the ring's first items: both in flight at once
     int mt = lane_token<TPG>();
     mt = mt < n_tok ? mt : 0;
     x_issue<KIND, XT, GPER>(xraw, (const XT*)ws.h + (int64_t)s_wp[wave][mt] * F, kh * GPER);
+    for (int k = 0; k < tp.nbuf - 1 && first + k < last; ++k) issue(first + k);
   }
-  for (int k = 0; k < tp.nbuf - 1 && first + k < last; ++k) issue(first + k);
   XRegs<KIND, TPG, GPER> X;
   x_finish<KIND, XT, TPG, GPER>(X, xraw);
 
   const DecodeRegs kr = decode_regs<KIND, MT>();
   // Each pair's outputs, rounded to the activation type, reduced and stored at the start of the next item, after
   // its barrier, which also makes the other column half's sums (double-buffered) visible: one barrier an item.
-  // With the combine in this kernel they go out as device-scope stores (written through the XCD's L2) for the
-  // block that combines them.
+  // With the combine in this kernel they go out as device-scope stores for the block that combines them.
   float pacc[TPG];
   int yrow = -1, pbuf = 0;
   auto store_y = [&]() {
@@ -875,7 +975,8 @@ __global__ __launch_bounds__(FRONT_WAVES * 64) void k_moe_tail(const uint8_t* __
   if (tid < last - first) {
     const int tile = (first + tid) % TILES;
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
-    if (__hip_atomic_fetch_add(&ws.cnt[tile], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == groups - 1)
+    if (__hip_atomic_fetch_add(&ws.cnt[tile * CTR_STRIDE], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+        groups - 1)
       s_comb[atomicAdd(&s_ncomb, 1)] = tile;
   }
   __syncthreads();
@@ -885,11 +986,194 @@ __global__ __launch_bounds__(FRONT_WAVES * 64) void k_moe_tail(const uint8_t* __
   for (int qv = tid; qv < ncomb * B * IT::ROWS; qv += NT) {
     const int c = qv / (B * IT::ROWS), rest = qv - c * (B * IT::ROWS);
     const int t = rest / IT::ROWS, row = s_comb[c] * IT::ROWS + rest % IT::ROWS;
-    combine_one<XT>(t, row, K, B, ws.gsh[t], out, [&](int p) {
+    combine_one<XT>(t, row, K, B, gsh[t], out, [&](int p) {
       return __hip_atomic_load(ws.y + (int64_t)p * D + row, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }, [&](int p) { return ws.w[p]; });
+    }, wsrc);
   }
-  if (tid < ncomb) __hip_atomic_store(&ws.cnt[s_comb[tid]], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (tid < ncomb)
+    __hip_atomic_store(&ws.cnt[s_comb[tid] * CTR_STRIDE], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+template <int KIND, typename XT, int TPG>
+__global__ __launch_bounds__(FRONT_WAVES * 64) void k_moe_tail(const uint8_t* __restrict__ down,
+                                                               const uint8_t* __restrict__ sh_down, int K, int B,
+                                                               TailPlan tp, const uint8_t* __restrict__ signed_tab,
+                                                               MoeWs ws, int combine, XT* __restrict__ out) {
+  constexpr int NT = FRONT_WAVES * 64;
+  const int P = B * K;
+  __shared__ int s_groups;
+  __shared__ int s_idx[MOE_MAX_PAIRS], s_gexp[MOE_MAX_PAIRS + 1];
+  __shared__ float s_w[MOE_MAX_PAIRS], s_gsh[MOE_MAX_TOKENS];
+  __shared__ int s_wp[FRONT_WAVES][16];
+  extern __shared__ u32x4 dyn[];
+  const uint32_t lds_base = SH_LDS_ADDR(dyn);
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  // the IQ3_S table (it waits on nothing), then the front's choice and groups in one trip
+  if constexpr (KIND == IQ3_S) {
+#pragma unroll
+    for (int i = 0; i < IQ3S_SIGNED_BYTES / 16 / NT; ++i) {
+      const int c0 = wave * 64 + i * NT;
+      lds_dma16(signed_tab, 16 * (c0 + lane), lds_base + 16 * c0);
+    }
+  }
+  if (tid == 0) s_groups = *ws.n_groups;
+  if (tid < P) {
+    s_idx[tid] = ws.idx[tid];
+    s_w[tid] = ws.w[tid];
+  }
+  if (tid <= P) s_gexp[tid] = ws.g_expert[tid];  // entries past the groups are never read
+  if (tid < B) s_gsh[tid] = ws.gsh[tid];
+  __syncthreads();  // (also waits for the table)
+  tail_items<KIND, XT, TPG>(blockIdx.x, gridDim.x, s_groups, s_idx,
+                            [&](int g) { return __builtin_amdgcn_readfirstlane(s_gexp[g]); },
+                            [&](int p) { return s_w[p]; }, s_gsh, down, sh_down, K, B, tp, ws, combine, out,
+                            s_wp);
+}
+
+// ---- the whole layer in one launch, for windows of few groups (the common shape, Q2_0). SWITCHED OFF (nothing
+// reaches it: sh_moe_set_one_launch refuses to switch it on): at 2 tokens of float16 it made an illegal memory
+// access whose cause is not found. Every block routes the
+// window; then its ticket, taken in the order blocks start, makes it a gate / up block (the first `nfront`) or a
+// down block. A down block owns 16 rows of the output for every group: its waves load those rows of their groups'
+// down weights at once (a wave the groups w, w + 8, w + 16, two at a time), wait until every group's gate / up is
+// out, read the groups' h rows, and combine the 16 rows in LDS. The blocks a down block waits on hold lower
+// tickets, so they started before it and wait on nothing: no order of dispatch or residency can make the wait
+// circular. The counters come in two sets used by calls in turn; every block reads which before it draws its
+// ticket, and the block that draws the last ticket clears the other set and switches to it for the next call.
+constexpr int LAYER_GROUPS = 3 * FRONT_WAVES;  // groups a window may have for the one launch
+constexpr int LAYER_PAIRS = 48;                // pairs and shared tokens (B * k + B) it may have
+constexpr int LAYER_ROWS = 16;                 // output rows a down block owns
+
+template <int KIND> struct RowSlot {  // a group's 16 rows of down weights in LDS, as they lie
+  static constexpr int RB = (int)row_bytes_dev(KIND, FRONT_F);
+  static constexpr int CHUNKS = LAYER_ROWS * RB / 16, LOADS = (CHUNKS + 63) / 64, SLOT = LOADS * 1024;
+};
+
+template <int KIND, typename XT, typename LT, int TPG>
+__global__ __launch_bounds__(FRONT_WAVES * 64) void k_moe_layer(
+    const uint8_t* __restrict__ gate, const uint8_t* __restrict__ up, const uint8_t* __restrict__ down,
+    const uint8_t* __restrict__ sh_gate, const uint8_t* __restrict__ sh_up, const uint8_t* __restrict__ sh_down,
+    const LT* __restrict__ logits, const XT* __restrict__ x, const XT* __restrict__ wgt, int K, int B, FrontPlan fp,
+    int row_off, int nfront, MoeWs ws, XT* __restrict__ out) {
+  static_assert(KIND == Q2_0, "the one-launch layer is written for Q2_0 gate, up and down");
+  using MT = XT;
+  using RS = RowSlot<KIND>;
+  constexpr int E = FRONT_E, D = FRONT_D, F = FRONT_F, NT = FRONT_WAVES * 64, GPER = F / 64;
+  constexpr int TW = FRONT_WAVES - 1;  // the ticket's wave: past the route's tokens for windows of few groups
+  __shared__ RouteLds<LT> r;
+  __shared__ int s_ticket, s_set;
+  __shared__ float s_gsh[MOE_MAX_TOKENS];
+  __shared__ int s_wp[LAYER_GROUPS][16];  // gate / up: a wave's group's pairs; down: each group's
+  __shared__ float s_y[LAYER_PAIRS][LAYER_ROWS];
+  extern __shared__ u32x4 dyn[];
+  uint8_t* lds = (uint8_t*)dyn;
+  const uint32_t lds_base = SH_LDS_ADDR(dyn);
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  // the counter set, read before the ticket is drawn; the ticket's value is used after the route (its wave issues
+  // no loads meanwhile, so nothing waits on the atomic until then)
+  int set = 0, ticket = 0;
+  if (tid == TW * 64) {
+    set = __hip_atomic_load(ws.par, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    ticket = __hip_atomic_fetch_add(ws.ticket, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  const RouteGroups rg = moe_route<LT>(logits, K, B, r);
+  if (tid == TW * 64) {
+    s_ticket = ticket;
+    s_set = set;
+  }
+  lds_sync();
+  ticket = s_ticket;
+  set = s_set;
+  if (ticket < 0 || ticket >= (int)gridDim.x || (set & ~1)) {  // counters not at zero: no work, nothing read past them
+    if (tid == 0) __hip_atomic_store(ws.err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return;
+  }
+  if (ticket == (int)gridDim.x - 1) {  // every block has read the set and drawn its ticket
+    const int other = set ^ 1;
+    for (int i = tid; i < MOE_MAX_PAIRS + 1; i += NT)
+      __hip_atomic_store(&ws.gdone[(other * (MOE_MAX_PAIRS + 1) + i) * CTR_STRIDE], 0, __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
+    if (tid < 8)
+      __hip_atomic_store(&ws.gflag[(other * 8 + tid) * CTR_STRIDE], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (tid == 0) {
+      __hip_atomic_store(&ws.gall[other * CTR_STRIDE], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(ws.ticket, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(ws.par, other, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
+  if (ticket < nfront) {
+    if (ticket == 0) {
+      route_publish<LT>(rg, r, B * K, ws, false);
+      shared_gate_logits<XT>(x, wgt, B, ws.gsh);
+    }
+    front_items<KIND, XT, LT, TPG>(ticket, nfront, rg, r, gate, up, sh_gate, sh_up, x, K, B, fp, ws, set + 1, s_wp);
+    return;
+  }
+  const int rt = ticket - nfront;  // block-uniform
+  if (rt >= D / LAYER_ROWS) return;
+  const int row0 = rt * LAYER_ROWS, groups = rg.groups;
+  const int ng = groups > wave ? (groups - wave + FRONT_WAVES - 1) / FRONT_WAVES : 0;  // this wave's groups
+  auto slot = [&](int j) { return row_off + (2 * wave + (j & 1)) * RS::SLOT; };
+  auto issue = [&](int j) {
+    const int e = group_expert(rg, wave + FRONT_WAVES * j);
+    const uint8_t* src = (e == E ? sh_down : down + (int64_t)e * D * RS::RB) + (int64_t)row0 * RS::RB;
+#pragma unroll
+    for (int c = 0; c < RS::LOADS; ++c)
+      lds_dma16(src, 16 * min(c * 64 + lane, RS::CHUNKS - 1), lds_base + slot(j) + c * 1024);
+  };
+  for (int j = 0; j < ng && j < 2; ++j) issue(j);
+  int n_tok[3];
+  for (int j = 0; j < 3; ++j)
+    n_tok[j] = j < ng ? group_pairs(group_expert(rg, wave + FRONT_WAVES * j), E, r.idx, B, K,
+                                    s_wp[wave + FRONT_WAVES * j])
+                      : 0;
+  shared_gate_logits<XT>(x, wgt, B, s_gsh);
+  if (tid == 0) {  // every group's h is out once this block's eighth of the flags is up
+    const int32_t* flag = ws.gflag + (set * 8 + (rt & 7)) * CTR_STRIDE;
+    int spins = 0;
+    while (__hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 0) {
+      __builtin_amdgcn_s_sleep(1);
+      if (++spins > MOE_MAX_SPINS) {
+        __hip_atomic_store(ws.err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        break;
+      }
+    }
+  }
+  lds_sync();  // (the slots' loads stay in flight)
+  const DecodeRegs kr = decode_regs<KIND, MT>();
+  for (int j = 0; j < ng; ++j) {
+    const int* wp = s_wp[wave + FRONT_WAVES * j];
+    int mt = lane_token<TPG>();
+    mt = mt < n_tok[j] ? mt : 0;
+    XRaw<KIND, GPER> xraw;
+    x_issue_agent<KIND, XT, GPER>(xraw, (const XT*)ws.h, wp[mt], F, 0);
+    XRegs<KIND, TPG, GPER> X;
+    x_finish<KIND, XT, TPG, GPER>(X, xraw);
+    wait_vmcnt(0);  // the slot's rows, loaded before h
+    float acc[TPG];
+#pragma unroll
+    for (int t = 0; t < TPG; ++t) acc[t] = 0.0f;
+    item_mac<KIND, MT, TPG, GPER, true>(lds + slot(j), RS::RB, X, nullptr, kr, acc);
+    const int q = lane >> 4, n = lane & 15;
+#pragma unroll
+    for (int t = 0; t < TPG; ++t) {
+      const int tt = q * TPG + t;
+      if (tt < n_tok[j]) s_y[wp[tt]][n] = to_f32(from_f32<XT>(acc[t]));
+    }
+    if (j == 0 && ng > 2) {  // the third group into the first one's slot, once this wave has read it
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      issue(2);
+    }
+  }
+  lds_sync();
+  if (tid < B * LAYER_ROWS) {
+    const int t = tid / LAYER_ROWS, n = tid % LAYER_ROWS;
+    combine_one<XT>(t, row0 + n, K, B, s_gsh[t], out, [&](int p) { return s_y[p][n]; },
+                    [&](int p) { return r.wt[p]; });
+  }
 }
 
 // The tail for a window of few groups (at most 16: one token's k experts and the shared one), Q2_0: a block is 16
@@ -1143,6 +1427,46 @@ static int launch_moe(const uint8_t* gate, const uint8_t* up, const uint8_t* dow
                       hipStream_t stream, int phases) {
   const uint8_t* stab = tables ? tables + TAB_IQ3S_SIGNED : nullptr;
   int st = OK;
+  if (phases & 32) {  // the whole layer in one launch (windows of few groups, Q2_0), else the two launches
+    if constexpr (KIND == Q2_0 && KIND_DOWN == Q2_0) {
+      const int64_t groups_most = std::min<int64_t>(B * K, E) + 1;
+      if (groups_most <= LAYER_GROUPS && B * K + B <= LAYER_PAIRS) {
+        using IF = FrontItem<KIND>;
+        using RS = RowSlot<KIND_DOWN>;
+        auto kern = k_moe_layer<KIND, XT, LT, TPG>;
+        const int nt = FRONT_WAVES * 64;
+        const size_t fixed = static_lds(kern);
+        const size_t red_f = (size_t)2 * 2 * 7 * 64 * TPG * 4;
+        const size_t rows = (size_t)2 * FRONT_WAVES * RS::SLOT;  // the down blocks' slots
+        FrontPlan fp;
+        fp.ring_off = 0;
+        // direct loads land below 128 KiB; a shallower ring where that makes room for two blocks a CU
+        fp.nbuf = 3;
+        while (fp.nbuf > 2 && ((size_t)fp.nbuf * IF::SLOT > 128 * 1024 ||
+                               fixed + (size_t)fp.nbuf * IF::SLOT + red_f > LDS_BYTES ||
+                               (fixed + (size_t)fp.nbuf * IF::SLOT + red_f > LDS_BYTES / 2 &&
+                                fixed + (size_t)(fp.nbuf - 1) * IF::SLOT + red_f <= LDS_BYTES / 2)))
+          --fp.nbuf;
+        fp.red_off = fp.nbuf * IF::SLOT;
+        const size_t lds = std::max((size_t)fp.red_off + red_f, rows);
+        if ((size_t)fp.red_off > 128 * 1024 || rows > 128 * 1024 || lds + fixed > LDS_BYTES)
+          return fail(E_UNSUPPORTED, "moe_decode: %zu bytes of LDS for the one-launch layer", lds);
+        int per_cu = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, nt, lds) != hipSuccess || per_cu < 1)
+          per_cu = 1;
+        // the down blocks first (a block a 16-row slice of the output), the gate / up blocks what is left of the
+        // blocks that fit at once, up to a block an item
+        const int64_t ndown = FRONT_D / LAYER_ROWS, fit = (int64_t)device_cus() * per_cu;
+        const int64_t nfront = std::min<int64_t>(groups_most * (FRONT_F / 16), fit - ndown);
+        if (nfront >= groups_most) {
+          hipLaunchKernelGGL(kern, dim3((unsigned)(nfront + ndown)), dim3(nt), lds, stream, gate, up, down, sg, su, sd,
+                             logits, x, wg, (int)K, (int)B, fp, 0, (int)nfront, ws, out);
+          return check_launch("moe_decode layer");
+        }
+      }
+    }
+    phases = 8 | 16;
+  }
   if (phases & 8) {  // front: route, gate and up (the common shape)
     using IT = FrontItem<KIND>;
     FrontPlan fp;
@@ -1289,7 +1613,11 @@ int moe_decode(int phases, int kind, int kind_down, const void* gate, const void
   const bool aligned = ((uintptr_t)gate | (uintptr_t)up | (uintptr_t)down | (uintptr_t)shared_gate |
                         (uintptr_t)shared_up | (uintptr_t)shared_down | (uintptr_t)x | (uintptr_t)shared_gate_w) % 16 == 0;
   if (experts == FRONT_E && d_model == FRONT_D && d_ff == FRONT_F && aligned) {
-    phases = (phases & 3 ? 8 : 0) | (phases & 4 ? 16 : 0);
+    // the whole step in one launch, or (kernel by kernel, or with the one-launch form off) front then tail
+    if (phases == 7 && g_one_launch.load(std::memory_order_relaxed))
+      phases = 32;
+    else
+      phases = (phases & 3 ? 8 : 0) | (phases & 4 ? 16 : 0);
   }
   const int tpg = tokens <= 4 ? 1 : tokens <= 8 ? 2 : 4;
   if (logits_dtype != F32 && logits_dtype != dtype)
@@ -1319,7 +1647,7 @@ int moe_decode(int phases, int kind, int kind_down, const void* gate, const void
     return kind == Q2_0 ? by_down(kind_c<Q2_0>{}) : by_down(kind_c<IQ3_S>{});
   });
   if (st) return st;
-  if (!(phases & 9)) return OK;  // the choice comes from the route or the front
+  if (!(phases & (9 | 32))) return OK;  // the choice comes from the route, the front or the one-launch layer
   if (idx_out && hipMemcpyAsync(idx_out, ws.idx, 4 * tokens * k, hipMemcpyDeviceToDevice, (hipStream_t)stream) != hipSuccess)
     return fail(E_HIP, "moe_decode: copy of the choice failed");
   if (w_out && hipMemcpyAsync(w_out, ws.w, 4 * tokens * k, hipMemcpyDeviceToDevice, (hipStream_t)stream) != hipSuccess)
@@ -1336,9 +1664,14 @@ constexpr int MAX_DEVICES = 64;
 static std::mutex g_scratch_mu;
 static void* g_scratch_at[MAX_DEVICES];  // the array's device address on each GPU, found once a GPU
 
+__global__ void k_clear_words(int32_t* p, int n) {
+  for (int i = threadIdx.x; i < n; i += blockDim.x) p[i] = 0;
+}
+
 // the current device's copy of `scratch`: its address comes from the runtime (the array's name in host code is a
-// stand-in, not a device address), looked up the first time a device calls and kept for it
-static int scratch_of(void** at) {
+// stand-in, not a device address), looked up the first time a device calls and kept for it; that first call also
+// clears the control words at its head on `stream` (every call after leaves them at zero)
+static int scratch_of(void** at, hipStream_t stream) {
   int dev = -1;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= MAX_DEVICES)
     return fail(E_HIP, "moe_decode_noalloc: no current device (%d)", dev);
@@ -1349,6 +1682,9 @@ static int scratch_of(void** at) {
     if (e != hipSuccess || !p)
       return fail(E_HIP, "moe_decode_noalloc: address of the scratch array on device %d: %s", dev,
                   hipGetErrorString(e));
+    hipLaunchKernelGGL(k_clear_words, dim3(1), dim3(256), 0, stream, (int32_t*)p, (int)(MOE_HEAD_BYTES / 4));
+    const int st = check_launch("moe_decode_noalloc clear");
+    if (st) return st;
     g_scratch_at[dev] = p;
   }
   *at = g_scratch_at[dev];
@@ -1375,9 +1711,8 @@ int sh_moe_decode_noalloc(int kind, int kind_down, const void* gate, const void*
   }
   if (tokens <= 0) return OK;
   void* ws = nullptr;
-  const int st = scratch_of(&ws);
+  const int st = scratch_of(&ws, (hipStream_t)stream);
   if (st) return st;
-  // nothing in the workspace has to start at zero: the first kernel of each call clears the tail's counters
   return moe_decode(7, kind, kind_down, gate, up, down, experts, shared_gate, shared_up, shared_down, shared_gate_w,
                     tables, logits, logits_dtype, x, dtype, tokens, k, d_model, d_ff, out, idx_out, w_out, ws,
                     MOE_SCRATCH_BYTES, stream);
@@ -1396,6 +1731,13 @@ int sh_moe_decode(int kind, int kind_down, const void* gate, const void* up, con
   return moe_decode(7, kind, kind_down, gate, up, down, experts, shared_gate, shared_up, shared_down, shared_gate_w,
                     tables, logits, logits_dtype, x, dtype, tokens, k, d_model, d_ff, out, idx_out, w_out, workspace,
                     workspace_bytes, stream);
+}
+
+int sh_moe_set_one_launch(int on) {
+  if (on)
+    return fail(E_UNSUPPORTED, "moe_set_one_launch: the one-launch layer is switched off (an illegal memory access at "
+                "2 tokens whose cause is not found)");
+  return g_one_launch.exchange(0);
 }
 
 int sh_moe_set_tail_combine(int upto) {

@@ -63,6 +63,22 @@ __device__ __forceinline__ void x_issue(XRaw<KIND, GPER>& R, const XT* xr, int g
   }
 }
 
+// the same loads of row `row` of `base` (row length `len`) written by other blocks of the launch (ld_agent16)
+template <int KIND, typename XT, int GPER>
+__device__ __forceinline__ void x_issue_agent(XRaw<KIND, GPER>& R, const XT* base, int row, int len, int gbase) {
+  const int g = (threadIdx.x & 63) >> 4;
+  const uint32_t r0 = (uint32_t)row * len * sizeof(XT);
+#pragma unroll
+  for (int j = 0; j < GPER; ++j) {
+    if constexpr (KIND == Q2_0) {
+      R.v[j][0] = ld_agent16(base, r0 + ((gbase + j) * 64 + 8 * g) * sizeof(XT));
+      R.v[j][1] = ld_agent16(base, r0 + ((gbase + j) * 64 + 32 + 8 * g) * sizeof(XT));
+    } else {
+      R.v[j][0] = ld_agent16(base, r0 + ((gbase + j) * 32 + 8 * g) * sizeof(XT));
+    }
+  }
+}
+
 // minus each group's offset sum for the TPG tokens of the lane's D-rows: the lane's share, added over the four
 // lanes of a row (xor 16, 32), then fetched from a lane whose A-row is the wanted token (lane 4g + t holds token
 // g * TPG + t)

@@ -126,6 +126,25 @@ __device__ __forceinline__ void lds_dma16p(const void* src, uint32_t lds) {
 // the LDS byte address of a __shared__ array (cast on the array itself: no null check of a generic pointer)
 #define SH_LDS_ADDR(arr) ((uint32_t)(uintptr_t)(__attribute__((address_space(3))) void*)(arr))
 
+// ---- data handed from block to block inside one launch: stores and loads with the agent-scope coherence bit (sc1),
+// which the chip keeps coherent across its XCDs' L2s as it keeps agent-scope atomics (they compile to the same
+// accesses). A writer's stores are complete once its vmcnt drains, so it waits for them and then counts; a reader
+// issues its loads after it has seen the count. No cache is written back or invalidated on either side: an
+// agent-scope fence would do both, over the whole L2 of its XCD, and a launch of hundreds of blocks that each fence
+// spends tens of microseconds on them.
+template <typename T> __device__ __forceinline__ void st_agent(T* p, T v) {
+  static_assert(sizeof(T) == 2 || sizeof(T) == 4, "st_agent: 16- or 32-bit values");
+  using U = std::conditional_t<sizeof(T) == 2, uint16_t, uint32_t>;
+  U bits;
+  __builtin_memcpy(&bits, &v, sizeof(T));
+  __hip_atomic_store((U*)p, bits, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// 16 bytes at base + off (base wave-uniform, off < 2^31), read at agent scope
+__device__ __forceinline__ u32x4 ld_agent16(const void* base, uint32_t off) {
+  const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, 0x7fffffff, 0x00020000);
+  return __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 16 /* sc1 */);
+}
+
 // at most n of this wave's memory loads still in flight (n wave-uniform; values above 63 wait for none)
 __device__ __forceinline__ void wait_vmcnt(int n) {
 #define SH_VMCNT_CASE(k) \

@@ -242,3 +242,59 @@ def test_the_tails_own_combine_gives_the_combine_kernels_bits(kinds, tokens, dty
     want, _, _ = OM.moe_decode_blocks(logits.float().cpu().numpy(), x.float().cpu().numpy(), K, fetch, kinds,
                                       (E, D, F), shared, wg.float().cpu().numpy(), tables, name)
     assert rel_err(in_tail.float().cpu(), want) <= 1e-2
+
+
+@pytest.mark.skip(reason="the one-launch layer is switched off: it made an illegal memory access at 2 tokens "
+                         "(Q2_0, float16) whose cause is not found; sh_moe_set_one_launch(1) is refused")
+@pytest.mark.parametrize("kinds", [("Q2_0", "Q2_0"), ("IQ3_S", "IQ3_S"), ("IQ3_S", "Q2_0")])
+@pytest.mark.parametrize("tokens", [1, 2, 4, 5, 8, 16])
+def test_one_launch_gives_the_two_kernels_bits(kinds, tokens, c3_layers, tables, dev):
+    """The common shape's step as one launch (gate / up and down blocks in one grid, down waiting on its group's
+    count) against the front and tail kernels launched one after the other: the same bits, call after call (the
+    counts the launch leaves behind are cleared for the next)."""
+    from strata_hip import _lib
+
+    E, D, F, K = 512, 2048, 512, 10
+    fetch, lin, shared = c3_layers[kinds]
+    rng = np.random.default_rng(tokens + 500)
+    x = torch.from_numpy(rng.standard_normal((tokens, D)).astype(np.float32)).to(torch.bfloat16).to(dev)
+    logits = torch.from_numpy(rng.standard_normal((tokens, E)).astype(np.float32)).to(dev)
+    wg = torch.from_numpy(rng.standard_normal(D).astype(np.float32) * 0.05).to(torch.bfloat16).to(dev)
+    moe = SF.MoEDecode(lin["gate"], lin["up"], lin["down"], lin["sgate"], lin["sup"], lin["sdown"], wg, K)
+    lib = _lib.load()
+    before = lib.sh_moe_set_one_launch(0)
+    try:
+        two, idx2, w2 = moe(logits, x, want_choice=True)
+        torch.cuda.synchronize()
+        lib.sh_moe_set_one_launch(1)
+        for _ in range(3):
+            one, idx1, w1 = moe(logits, x, want_choice=True)
+            torch.cuda.synchronize()
+            assert torch.equal(one, two) and torch.equal(idx1, idx2) and torch.equal(w1, w2)
+    finally:
+        lib.sh_moe_set_one_launch(before)
+    want, _, _ = OM.moe_decode_blocks(logits.cpu().numpy(), x.float().cpu().numpy(), K, fetch, kinds, (E, D, F),
+                                      shared, wg.float().cpu().numpy(), tables, "bfloat16")
+    assert rel_err(one.float().cpu(), want) <= 1e-2
+
+
+@pytest.mark.parametrize("kinds", [("Q2_0", "Q2_0"), ("IQ3_S", "Q2_0")])
+def test_one_workspace_serves_every_token_count(kinds, c3_layers, tables, dev):
+    """One zeroed workspace, sized for 16 tokens, passed to calls of 16, 2, 8, 1 and 5 tokens in turn: the launch's
+    counters sit at the workspace's head whatever the shape, so each call starts from the zeros the one before
+    left, and gives the bits of a call with a workspace of its own."""
+    E, D, F, K = 512, 2048, 512, 10
+    fetch, lin, shared = c3_layers[kinds]
+    wg = (torch.randn(D, device=dev, generator=torch.Generator(device=dev).manual_seed(9)) * 0.05).to(torch.bfloat16)
+    fresh = SF.MoEDecode(lin["gate"], lin["up"], lin["down"], lin["sgate"], lin["sup"], lin["sdown"], wg, K)
+    shared_ws = SF.MoEDecode(lin["gate"], lin["up"], lin["down"], lin["sgate"], lin["sup"], lin["sdown"], wg, K)
+    big = fresh.workspace(16, torch.bfloat16, dev).clone()
+    shared_ws.workspace = lambda tokens, dtype, device: big
+    rng = np.random.default_rng(77)
+    for tokens in (16, 2, 8, 1, 5):
+        x = torch.from_numpy(rng.standard_normal((tokens, D)).astype(np.float32)).to(torch.bfloat16).to(dev)
+        logits = torch.from_numpy(rng.standard_normal((tokens, E)).astype(np.float32)).to(dev)
+        want, want_idx, want_w = fresh(logits, x, want_choice=True)
+        got, idx, w = shared_ws(logits, x, want_choice=True)
+        torch.cuda.synchronize()
+        assert torch.equal(got, want) and torch.equal(idx, want_idx) and torch.equal(w, want_w), tokens

@@ -56,3 +56,14 @@ def test_shape_errors_are_reported_before_any_launch():
     assert st == -2 and b"do not end on a block" in lib.sh_last_error()
     st = lib.sh_top_k(1, 0, 4, 4096, 10, 1, None, None)
     assert st == -2
+
+
+def test_the_one_launch_layer_cannot_be_switched_on():
+    """The one-launch MoE layer is switched off (an illegal memory access at 2 tokens whose cause is not found):
+    asking for it is refused on the host, and the setting stays off."""
+    from strata_hip import _lib
+
+    lib = _lib.load()
+    assert lib.sh_moe_set_one_launch(0) == 0
+    assert lib.sh_moe_set_one_launch(1) == -7 and b"switched off" in lib.sh_last_error()
+    assert lib.sh_moe_set_one_launch(0) == 0
