@@ -112,6 +112,19 @@ int sh_lookup_down_glu(const void* blocks, int64_t experts, int64_t rows, int64_
 int sh_router_matvec(const void* w, int w_dtype, int64_t rows, int64_t cols, const void* x, int x_dtype,
                      int64_t tokens, float* out, void* stream);
 
+/* strata_mlx/fused.py:281-323 (FusedResidual.__call__; kernels _NORM, _DOWN, _UP at 46-131): the hyper-connection
+ * read of a window of tokens <= 16 with the write before it. before (tokens x hc * d), out (tokens x d), inject_in
+ * (tokens x hc) in `dtype` (F32 / F16 / BF16); norm float32 (hc * d); down (rank x hc * d), up (hc * d x rank),
+ * inject_w (n_inject x hc * d, n_inject 0 or hc) in `w_dtype`, 16-byte aligned. Writes residual (tokens x hc * d:
+ * before + out * inject_in), mixed (tokens x d: the block's input) and, with inject rows, inject (tokens x hc: 2
+ * sigmoid of the inject rows' gate); sums in float32. hc 1, 2, 4 or 8; d a multiple of 64; rank 32..512 a
+ * multiple of 32. workspace: sh_hc_workspace() bytes. */
+size_t sh_hc_workspace(int64_t tokens, int64_t hc, int64_t d, int64_t rank, int64_t n_inject);
+int sh_hc_residual(const void* before, const void* out, const void* inject_in, int dtype, const void* norm,
+                   const void* down, const void* up, const void* inject_w, int w_dtype, int64_t tokens, int64_t hc,
+                   int64_t d, int64_t rank, int64_t n_inject, float eps, void* residual, void* mixed, void* inject,
+                   void* workspace, size_t workspace_bytes, void* stream);
+
 /* strata_mlx/fused.py:424-436 (top_k, kernel _TOPK 400-418) and 491 (softmax of the chosen logits):
  * idx (rows x k) of the k largest, largest first, ties to the lower index; weights (nullable) float32. */
 int sh_top_k(const void* logits, int dtype, int64_t rows, int64_t n, int64_t k, int32_t* idx, float* weights,

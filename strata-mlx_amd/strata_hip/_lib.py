@@ -33,6 +33,9 @@ PROTOTYPES = {
     "sh_lookup_matvec": [c_vp, c_i64, c_i64, c_i64, c_vp, c_i64, c_vp, c_int, c_i64, c_vp, c_vp],
     "sh_lookup_down_glu": [c_vp, c_i64, c_i64, c_i64, c_vp, c_i64, c_vp, c_vp, c_int, c_vp, c_vp],
     "sh_router_matvec": [c_vp, c_int, c_i64, c_i64, c_vp, c_int, c_i64, c_vp, c_vp],
+    "sh_hc_workspace": [c_i64, c_i64, c_i64, c_i64, c_i64],
+    "sh_hc_residual": [c_vp, c_vp, c_vp, c_int, c_vp, c_vp, c_vp, c_vp, c_int, c_i64, c_i64, c_i64, c_i64, c_i64,
+                       ctypes.c_float, c_vp, c_vp, c_vp, c_vp, c_sz, c_vp],
     "sh_top_k": [c_vp, c_int, c_i64, c_i64, c_i64, c_vp, c_vp, c_vp],
     "sh_moe_combine": [c_vp, c_vp, c_vp, c_vp, c_int, c_i64, c_i64, c_i64, c_vp, c_vp],
     "sh_tiles_workspace": [c_i64],
@@ -71,7 +74,7 @@ PROTOTYPES = {
 }
 _RESTYPE = {"sh_last_error": ctypes.c_char_p, "sh_tables_bytes": c_sz, "sh_tiles_workspace": c_sz,
             "sh_tiles_most": c_i64, "sh_switch_workspace": c_sz,
-            "sh_moe_workspace": c_sz, "sh_stack_workspace": c_sz, "sh_paged_attn_workspace": c_sz,
+            "sh_moe_workspace": c_sz, "sh_hc_workspace": c_sz, "sh_stack_workspace": c_sz, "sh_paged_attn_workspace": c_sz,
             "sh_cells_attn_workspace": c_sz, "sh_moe_scratch_bytes": c_sz}
 
 _lib = None

@@ -67,3 +67,17 @@ def test_the_one_launch_layer_cannot_be_switched_on():
     assert lib.sh_moe_set_one_launch(0) == 0
     assert lib.sh_moe_set_one_launch(1) == -7 and b"switched off" in lib.sh_last_error()
     assert lib.sh_moe_set_one_launch(0) == 0
+
+
+def test_hyper_connection_shapes_are_checked_before_any_launch():
+    from strata_hip import _lib
+
+    lib = _lib.load()
+    assert lib.sh_hc_workspace(8, 4, 2560, 128, 4) > 8 * 4 * 2560 * 4  # normed, partial sums, low-rank values
+    p = 16
+    # 17 tokens, 3 streams, rank 48, inject rows that are not the streams: each refused on the host
+    for args, what in (((17, 4, 128, 32, 4), b"tokens"), ((2, 3, 128, 32, 3), b"streams"),
+                       ((2, 4, 96, 32, 4), b"multiple of 64"), ((2, 4, 128, 48, 4), b"rank"),
+                       ((2, 4, 128, 32, 2), b"inject rows")):
+        st = lib.sh_hc_residual(p, p, p, 1, p, p, p, p, 1, *args, 1e-6, p, p, p, p, 1 << 30, None)
+        assert st == -2 and what in lib.sh_last_error(), (args, lib.sh_last_error())
