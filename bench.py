@@ -13,14 +13,30 @@ tokens actually chose (counted from the routing) plus the shared expert, plus ac
 roofline: the dominant kernel, k_moe_front (route, then gate/up with SwiGLU: two thirds of the expert bytes), its
 launches timed by HIP events around a graph of them alone; its algorithmic bytes are the gate and up blocks of the
 chosen and the shared experts, the logits and hidden states in, swiglu(gate, up) out. traffic: the HBM bytes a
-launch moves by the FETCH_SIZE / WRITE_SIZE counters (profiles/moe_front_traffic.json, made by
-strata-mlx_amd/strata_hip/profile_traffic.py under rocprofv3). cpu_baseline: the numpy oracle's restatement of the
-reference's dequantize + matmul path on the host, one thread, over a bounded sample of the same layers.
+launch moves by the FETCH_SIZE / WRITE_SIZE counters (profiles/moe_front_traffic.json), reported only when that
+summary was read on this source of the kernel (its hash of csrc/moe.hip matches), else null. cpu_baseline: the numpy
+oracle's restatement of the reference's dequantize + matmul path on the host, over a bounded sample of the same
+layers, on one thread and on all cores.
 
     python bench.py [--steps K] [--warmup W] [--layers 48] [--batches 1,2,4,8] [--no-cpu]
+
+The counter summary (two runs under rocprofv3, one counter each, then the summary; R the repository root, OUT an
+output directory, from /tmp with TMPDIR=/tmp):
+
+    rocprofv3 --pmc FETCH_SIZE --output-format csv -d $OUT/fetch -o f -- python3 $R/bench.py --traffic-run
+    rocprofv3 --pmc WRITE_SIZE --output-format csv -d $OUT/write -o w -- python3 $R/bench.py --traffic-run
+    python3 $R/bench.py --traffic-summarize $OUT > $R/profiles/moe_front_traffic.json
+
+--traffic-run first copies 256 MiB device to device (hipMemcpyAsync's copy kernel: 256 MiB read, 256 MiB written,
+the counters' calibration), then launches the front of the benchmark's layer over 48 distinct layers at each batch
+1, 2, 4, 8; --traffic-summarize scales each counter by what it read for the copy and reports the bytes a front
+launch moves.
 """
 
 import argparse
+import csv
+import glob
+import hashlib
 import json
 import os
 import sys
@@ -47,14 +63,101 @@ def front_bytes(u: int, b: int, expert_bytes: int = EXPERT_BYTES) -> int:
     return (u + 1) * 2 * expert_bytes // 3 + b * E * 2 + b * D * 2 + (b * K + b) * F * 2
 
 
+MOE_SOURCE = os.path.join(ROOT, "strata-mlx_amd", "csrc", "moe.hip")
+TRAFFIC_JSON = os.path.join(ROOT, "profiles", "moe_front_traffic.json")
+COPY_BYTES = 256 * 2**20
+TRAFFIC_BATCHES = (1, 2, 4, 8)
+
+
+def source_hash() -> str:
+    with open(MOE_SOURCE, "rb") as f:
+        return hashlib.sha256(f.read()).hexdigest()
+
+
 def front_traffic():
-    """HBM bytes a k_moe_front launch moves, averaged over the batches the counters were read at (None without the
-    committed counter summary)."""
-    path = os.path.join(ROOT, "profiles", "moe_front_traffic.json")
-    if not os.path.exists(path):
+    """HBM bytes a k_moe_front launch moves, averaged over the batches the counters were read at; None without the
+    committed counter summary or when it was read on another source of the kernel."""
+    if not os.path.exists(TRAFFIC_JSON):
         return None
-    with open(path) as f:
-        return json.load(f).get("traffic_bytes_per_launch")
+    with open(TRAFFIC_JSON) as f:
+        summary = json.load(f)
+    if summary.get("source_sha256") != source_hash():
+        print("# traffic: the counter summary was read on another source of csrc/moe.hip; reported as null",
+              file=sys.stderr)
+        return None
+    return summary.get("traffic_bytes_per_launch")
+
+
+def traffic_run():
+    """The workload the two counter runs read: the calibration copy, then the front launches."""
+    import torch
+
+    import strata_hip
+    from strata_hip import fused as SF
+    from strata_hip import tables as T
+
+    strata_hip.load()
+    T.use(T.synthetic(0))
+    dev = torch.device("cuda:0")
+    src = torch.empty(COPY_BYTES, dtype=torch.uint8, device=dev).fill_(1)
+    dst = torch.empty_like(src)
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    layers, _ = build_layers(48, dev, "Q2_0")
+    algo = {}
+    for b in TRAFFIC_BATCHES:
+        g = torch.Generator(device=dev)
+        g.manual_seed(1000 + b)
+        lg = [torch.randn(b, E, device=dev, generator=g).to(torch.bfloat16) for _ in layers]
+        xs = [torch.randn(b, D, device=dev, generator=g).to(torch.bfloat16) for _ in layers]
+        uniq = [int(torch.unique(SF.top_k(l, K)).numel()) for l in lg]
+        for m, l, x in zip(layers, lg, xs):
+            m(l, x, phase=1)
+        torch.cuda.synchronize()
+        algo[b] = sum(front_bytes(u, b) for u in uniq) / len(uniq)
+        print(f"B={b}: front launches {len(layers)}, algorithmic bytes a launch {algo[b]:.0f}", flush=True)
+    print(json.dumps({"algorithmic_bytes_per_launch": algo}), flush=True)
+
+
+def _counters(d, name):
+    """[(dispatch id, kernel name, value)] of counter `name` in a rocprofv3 csv directory, in dispatch order"""
+    out = []
+    for f in glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True):
+        for r in csv.DictReader(open(f)):
+            if r["Counter_Name"] == name:
+                out.append((int(r["Dispatch_Id"]), r["Kernel_Name"], float(r["Counter_Value"])))
+    return sorted(out)
+
+
+def traffic_summarize(d):
+    fetch, write = _counters(os.path.join(d, "fetch"), "FETCH_SIZE"), _counters(os.path.join(d, "write"), "WRITE_SIZE")
+    cf = next(v for _, k, v in fetch if "copyBuffer" in k)  # the copy: 256 MiB read and 256 MiB written
+    cw = next(v for _, k, v in write if "copyBuffer" in k)
+    kf, kw = COPY_BYTES / cf, COPY_BYTES / cw
+    f = [v for _, k, v in fetch if "k_moe_front" in k]
+    w = [v for _, k, v in write if "k_moe_front" in k]
+    if not f or len(f) != len(w) or len(f) % len(TRAFFIC_BATCHES):
+        raise SystemExit(f"k_moe_front dispatches: {len(f)} read, {len(w)} written")
+    per = {}
+    n = len(f) // len(TRAFFIC_BATCHES)  # in launch order: 48 a batch
+    for i, b in enumerate(TRAFFIC_BATCHES):
+        per[str(b)] = {"fetch_bytes": round(sum(f[i * n:(i + 1) * n]) / n * kf),
+                       "write_bytes": round(sum(w[i * n:(i + 1) * n]) / n * kw)}
+    mean = sum(v["fetch_bytes"] + v["write_bytes"] for v in per.values()) / len(per)
+    print(json.dumps({
+        "kernel": "k_moe_front", "source_sha256": source_hash(),
+        "workload": "MoE layer front, 512 experts, d_model 2048, ffn 512, Q2_0, top-10, 48 distinct layers at each "
+                    "batch 1, 2, 4, 8",
+        "counters": "rocprofv3 --pmc FETCH_SIZE, then --pmc WRITE_SIZE (KiB a dispatch)",
+        "commands": ["cd /tmp && export TMPDIR=/tmp  (R: the repository root, OUT: an output directory)",
+                     "rocprofv3 --pmc FETCH_SIZE --output-format csv -d $OUT/fetch -o f -- python3 $R/bench.py "
+                     "--traffic-run",
+                     "rocprofv3 --pmc WRITE_SIZE --output-format csv -d $OUT/write -o w -- python3 $R/bench.py "
+                     "--traffic-run",
+                     "python3 $R/bench.py --traffic-summarize $OUT"],
+        "calibration": {"copy_bytes": COPY_BYTES, "fetch_kib_read": cf, "write_kib_read": cw,
+                        "fetch_scale": kf, "write_scale": kw},
+        "per_batch": per, "traffic_bytes_per_launch": round(mean)}, indent=1))
 
 
 def build_layers(n_layers, dev, kind):
@@ -436,7 +539,13 @@ def main():
     ap.add_argument("--no-attention", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-iq3s", action="store_true")
+    ap.add_argument("--traffic-run", action="store_true", help="the counter runs' workload (under rocprofv3)")
+    ap.add_argument("--traffic-summarize", metavar="DIR", help="the counter summary of two runs' output directory")
     args = ap.parse_args()
+    if args.traffic_run:
+        return traffic_run()
+    if args.traffic_summarize:
+        return traffic_summarize(args.traffic_summarize)
     if args.gpus != 1:
         print(f"bench.py: --gpus {args.gpus}: this path runs and is measured on one GPU (expert parallelism across "
               f"GPUs is not implemented); run with --gpus 1", file=sys.stderr)
