@@ -179,8 +179,8 @@ int sh_moe_decode_noalloc(int kind, int kind_down, const void* gate, const void*
 int sh_moe_set_tail_combine(int upto);
 /* No counterpart in the reference: whether sh_moe_decode runs the common shape's step (512 experts, d_model 2048,
  * d_ff 512) as one launch (gate / up and down blocks in one grid) instead of two. The one-launch form is switched
- * off: on = 1 is refused with SH_E_UNSUPPORTED (it made an illegal memory access at 2 tokens whose cause is not
- * found); on = 0 returns the previous setting (0). */
+ * off: on = 1 is refused with SH_E_UNSUPPORTED (it made an illegal memory access at 2 tokens; the cause is fixed,
+ * the fix not yet run on a GPU); on = 0 returns the previous setting (0). */
 int sh_moe_set_one_launch(int on);
 /* One of sh_moe_decode's kernels alone (phase 0 route, 1 gate/up, 2 down + combine; for the two-kernel shape
  * phases 0 and 1 are both the route + gate/up kernel), in that order over one workspace: what a caller times or

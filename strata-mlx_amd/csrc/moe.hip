@@ -436,8 +436,10 @@ constexpr int TAIL_COMBINE_UPTO = 4;  // tokens up to which the tail combines in
 // the same bound as set at run time (sh_moe_set_tail_combine): 0 sends every window to the combine kernel
 static std::atomic<int> g_tail_combine_upto{TAIL_COMBINE_UPTO};
 // whether the common shape's step runs as one launch (sh_moe_set_one_launch). Off, and it cannot be switched on:
-// the one-launch layer (k_moe_layer) made an illegal memory access at 2 tokens (Q2_0, float16) whose cause is not
-// found; until it is, every window takes the two launches.
+// the one-launch layer (k_moe_layer) made an illegal memory access at 2 tokens (Q2_0, float16). The cause found
+// since (its direct loads read a base address that v_readfirstlane had just written, inside the hazard window that
+// lds_dma16 now waits out) is fixed, but the fix has not run on a GPU: until it has, every window takes the two
+// launches.
 static std::atomic<int> g_one_launch{0};
 
 // the pairs of group expert e in token order, into this wave's wp[0, n): pair t * K + j of each token t choosing e
@@ -1033,7 +1035,8 @@ __global__ __launch_bounds__(FRONT_WAVES * 64) void k_moe_tail(const uint8_t* __
 
 // ---- the whole layer in one launch, for windows of few groups (the common shape, Q2_0). SWITCHED OFF (nothing
 // reaches it: sh_moe_set_one_launch refuses to switch it on): at 2 tokens of float16 it made an illegal memory
-// access whose cause is not found. Every block routes the
+// access, from direct loads issued inside the wait-state window after v_readfirstlane wrote their base (lds_dma16
+// now waits it out); it stays off until that fix has run on a GPU. Every block routes the
 // window; then its ticket, taken in the order blocks start, makes it a gate / up block (the first `nfront`) or a
 // down block. A down block owns 16 rows of the output for every group: its waves load those rows of their groups'
 // down weights at once (a wave the groups w, w + 8, w + 16, two at a time), wait until every group's gate / up is
@@ -1736,7 +1739,7 @@ int sh_moe_decode(int kind, int kind_down, const void* gate, const void* up, con
 int sh_moe_set_one_launch(int on) {
   if (on)
     return fail(E_UNSUPPORTED, "moe_set_one_launch: the one-launch layer is switched off (an illegal memory access at "
-                "2 tokens whose cause is not found)");
+                "2 tokens; its cause is fixed but the fix has not run on a GPU)");
   return g_one_launch.exchange(0);
 }
 

@@ -109,19 +109,28 @@ __device__ __forceinline__ int lead_of(const void* p) { return (int)((uintptr_t)
 // any other; readers wait with wait_vmcnt and meet at lds_sync. Issued from inline assembly: the compiler's wait
 // insertion, which would count such a load as pending on the LDS counter too and then wait for every LDS read at
 // once, does not see it (its own waits on younger loads stay correct: the counter drains in order).
+//
+// The wait states the hardware needs before such a load are in the assembly itself, since the compiler inserts none
+// for an inline-assembly instruction: a VMEM instruction reading an SGPR that a VALU instruction wrote needs 5 (the
+// base, when the compiler computed it in vector registers, is moved to SGPRs by v_readfirstlane just before), and
+// an LDS direct load needs 1 after M0 is written (the compiler writes M0 just before). Without them the load can
+// take a stale base or LDS address: the two kernels that issued loads in that state ended in illegal memory
+// accesses.
 __device__ __forceinline__ void lds_dma16(const void* base, uint32_t off, uint32_t lds) {
   // the base is wave-uniform by contract: read from the first lane, it is a scalar operand whatever the compiler
   // could prove
   const uint64_t b = (uint64_t)(uintptr_t)base;
   const uint64_t sb = ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(b >> 32)) << 32) |
                       (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)b);
-  asm volatile("global_load_lds_dwordx4 %0, %1" ::"v"(off), "s"((const void*)(uintptr_t)sb),
+  asm volatile("s_nop 4\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off), "s"((const void*)(uintptr_t)sb),
                "{m0}"(__builtin_amdgcn_readfirstlane(lds))
                : "memory");
 }
-// the same with a full address a lane (sources in different tensors within one wave's load)
+// the same with a full address a lane (sources in different tensors within one wave's load): no SGPR operand, the
+// wait state after M0's write
 __device__ __forceinline__ void lds_dma16p(const void* src, uint32_t lds) {
-  asm volatile("global_load_lds_dwordx4 %0, off" ::"v"(src), "{m0}"(__builtin_amdgcn_readfirstlane(lds)) : "memory");
+  asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "{m0}"(__builtin_amdgcn_readfirstlane(lds))
+               : "memory");
 }
 // the LDS byte address of a __shared__ array (cast on the array itself: no null check of a generic pointer)
 #define SH_LDS_ADDR(arr) ((uint32_t)(uintptr_t)(__attribute__((address_space(3))) void*)(arr))

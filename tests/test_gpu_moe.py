@@ -245,7 +245,9 @@ def test_the_tails_own_combine_gives_the_combine_kernels_bits(kinds, tokens, dty
 
 
 @pytest.mark.skip(reason="the one-launch layer is switched off: it made an illegal memory access at 2 tokens "
-                         "(Q2_0, float16) whose cause is not found; sh_moe_set_one_launch(1) is refused")
+                         "(Q2_0, float16); the cause (direct loads inside the wait-state window after "
+                         "v_readfirstlane wrote their base) is fixed but not yet run on a GPU; "
+                         "sh_moe_set_one_launch(1) is refused")
 @pytest.mark.parametrize("kinds", [("Q2_0", "Q2_0"), ("IQ3_S", "IQ3_S"), ("IQ3_S", "Q2_0")])
 @pytest.mark.parametrize("tokens", [1, 2, 4, 5, 8, 16])
 def test_one_launch_gives_the_two_kernels_bits(kinds, tokens, c3_layers, tables, dev):

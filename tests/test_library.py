@@ -59,8 +59,8 @@ def test_shape_errors_are_reported_before_any_launch():
 
 
 def test_the_one_launch_layer_cannot_be_switched_on():
-    """The one-launch MoE layer is switched off (an illegal memory access at 2 tokens whose cause is not found):
-    asking for it is refused on the host, and the setting stays off."""
+    """The one-launch MoE layer is switched off until its fault's fix has run on a GPU: asking for it is refused on
+    the host, and the setting stays off."""
     from strata_hip import _lib
 
     lib = _lib.load()
