@@ -19,6 +19,15 @@ from .blocks import BLOCK, _kind, _on_gpu, _tabs, _u8, dequantize, row_bytes, wi
 MAX_TOKENS = 8  # dense.py:33: more than a window is a chunk of a prompt, multiplied as floats
 AS_BLOCKS = ("Q3_K", "IQ4_XS")  # dense.py:189
 
+_holding = []  # dense.py:85: the layers holding their weights as floats as well, since a prompt was read
+
+
+def release():
+    """Let go of the float weights made for chunks of prompts (dense.py:88-94); nothing calls this by itself."""
+    for layer in _holding:
+        layer._floats = None
+    _holding.clear()
+
 
 def as_blocks(shape: tuple, kind: str, kinds: tuple = AS_BLOCKS) -> bool:
     """Whether a dense tensor of `shape` and `kind` can stay blocks (dense.py:193-195)."""
@@ -158,6 +167,8 @@ class ScaledLinear:
                 return x @ self.floats(x.dtype).T
             if self._floats is None or self._floats.dtype != x.dtype:
                 self._floats = self.floats(x.dtype)
+                if self not in _holding:
+                    _holding.append(self)
             return x @ self._floats.T
         xs = x.reshape(tokens, cols).contiguous()
         _on_gpu(self.codes, xs)
