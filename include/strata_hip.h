@@ -258,10 +258,12 @@ int sh_qk_rope(const void* x, int dtype, int64_t tokens, int64_t heads, int64_t 
 
 /* attention.py:251 (`cache.update_and_fetch(k, v)` of a paged cache): the window's keys and values k, v (n_new,
  * hkv, head_dim) written at positions pos0 .. pos0 + n_new - 1, position p to page page_table[p / 16], slot p % 16
- * of the pools (n_pages, hkv, 16, head_dim). Page ids outside 0..n_pages-1 are not written. Trimming rejected
+ * of the pools (n_pages, hkv, 16, head_dim). page_table holds table_pages entries: positions past 16 table_pages
+ * are refused with SH_E_SHAPE. Page ids outside 0..n_pages-1 are not written. Trimming rejected
  * drafts is the caller's position count alone (the pages keep what they hold until written again). */
 int sh_kv_append(const void* k, const void* v, int64_t n_new, int64_t hkv, int64_t head_dim, int dtype, void* k_pages,
-                 void* v_pages, const int32_t* page_table, int64_t n_pages, int64_t pos0, void* stream);
+                 void* v_pages, const int32_t* page_table, int64_t table_pages, int64_t n_pages, int64_t pos0,
+                 void* stream);
 
 /* _gathered in its own form (attention.py:132-165): query s attends to the n_cells cells cells[s] (int32, rows of
  * k / v (hkv, kv_len, head_dim)) whose flag real[s] (uint8) is set; q (n_q, hq, head_dim) -> out (n_q, hq,

@@ -115,11 +115,15 @@ int sh_qk_rope(const void* x, int dtype, int64_t tokens, int64_t heads, int64_t 
 }
 
 int sh_kv_append(const void* k, const void* v, int64_t n_new, int64_t hkv, int64_t head_dim, int dtype, void* k_pages,
-                 void* v_pages, const int32_t* page_table, int64_t n_pages, int64_t pos0, void* stream) {
+                 void* v_pages, const int32_t* page_table, int64_t table_pages, int64_t n_pages, int64_t pos0,
+                 void* stream) {
   if (n_new <= 0) return OK;
   if (hkv <= 0 || head_dim <= 0 || (head_dim * dtype_size(dtype)) % 16 || pos0 < 0 || n_pages <= 0)
     return fail(E_SHAPE, "kv_append: %lld KV heads of %lld at position %lld", (long long)hkv, (long long)head_dim,
                 (long long)pos0);
+  if (table_pages <= 0 || pos0 + n_new > table_pages * 16)
+    return fail(E_SHAPE, "kv_append: positions %lld .. %lld past a page table of %lld pages", (long long)pos0,
+                (long long)(pos0 + n_new - 1), (long long)table_pages);
   if (dtype != F16 && dtype != BF16 && dtype != F32) return fail(E_DTYPE, "kv_append: dtype %d", dtype);
   if (!k || !v || !k_pages || !v_pages || !page_table) return fail(E_ARG, "kv_append: null pointer");
   if (((uintptr_t)k | (uintptr_t)v | (uintptr_t)k_pages | (uintptr_t)v_pages) & 15)

@@ -67,7 +67,7 @@ PROTOTYPES = {
     "sh_cells_attn_paged": [c_vp, c_vp, c_vp, c_vp, c_i64, c_vp, c_vp, c_i64, c_i64, c_i64, c_i64, c_i64,
                             ctypes.c_float, c_int, c_vp, c_i64, c_i64, c_vp, c_vp, c_sz, c_vp],
     "sh_qk_rope": [c_vp, c_int, c_i64, c_i64, c_i64, c_i64, c_vp, ctypes.c_float, c_vp, c_vp, c_i64, c_vp, c_int, c_vp],
-    "sh_kv_append": [c_vp, c_vp, c_i64, c_i64, c_i64, c_int, c_vp, c_vp, c_vp, c_i64, c_i64, c_vp],
+    "sh_kv_append": [c_vp, c_vp, c_i64, c_i64, c_i64, c_int, c_vp, c_vp, c_vp, c_i64, c_i64, c_i64, c_vp],
     "sh_cells_attn_workspace": [c_i64, c_i64, c_i64, c_i64, c_i64],
     "sh_cells_attn": [c_vp, c_vp, c_vp, c_i64, c_vp, c_vp, c_i64, c_i64, c_i64, c_i64, c_i64, ctypes.c_float, c_int,
                       c_vp, c_vp, c_sz, c_vp],

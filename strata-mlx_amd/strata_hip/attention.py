@@ -165,7 +165,7 @@ class PagedKVCache:
         k, v = k.to(self.k_pages.dtype).contiguous(), v.to(self.k_pages.dtype).contiguous()
         _lib.call("sh_kv_append", k.data_ptr(), v.data_ptr(), S, hkv, D, _lib.dtype_code(k.dtype),
                   self.k_pages.data_ptr(), self.v_pages.data_ptr(), self.page_table.data_ptr(),
-                  self.k_pages.shape[0], self.offset, _lib.stream_of(k))
+                  self.page_table.numel(), self.k_pages.shape[0], self.offset, _lib.stream_of(k))
         self.offset += S
         return self.k_pages, self.v_pages
 
