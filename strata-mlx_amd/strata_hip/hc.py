@@ -66,8 +66,9 @@ class FusedResidual:
         b = before.reshape(T, self.wide).contiguous()
         o = out.reshape(T, self.d).to(dtype).contiguous()
         i = inject_in.reshape(T, self.hc).to(dtype).contiguous()
-        if self.down.device != b.device:
-            raise ValueError(f"FusedResidual: weights on {self.down.device}, activations on {b.device}")
+        for w in (self.norm, self.down, self.up, self.inject_w):
+            if w is not None and w.device != b.device:
+                raise ValueError(f"FusedResidual: weights on {w.device}, activations on {b.device}")
         n_inject = self.hc if self.inject_w is not None else 0
         residual = torch.empty_like(b)
         mixed = torch.empty((T, self.d), dtype=dtype, device=b.device)

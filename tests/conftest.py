@@ -23,16 +23,42 @@ def tables():
     return t
 
 
+HOSTRUN = os.environ.get("STRATA_HOSTRUN") == "1"
+
+
 @pytest.fixture(scope="session")
 def dev():
     import torch
 
+    if HOSTRUN:
+        return _host_device()
     if not torch.cuda.is_available():
         pytest.skip("no GPU")
     from strata_hip import _lib
 
     _lib.load()  # fail loudly if the library is not built
     return torch.device("cuda:0")
+
+
+def _host_device():
+    """STRATA_HOSTRUN=1: the GPU tests run on the CPU against the host build of the same kernels (tests/hostrun),
+    with CPU tensors standing for device memory. A check of the kernels' arithmetic and addressing where no GPU is
+    at hand; the package itself only ever loads the HIP library."""
+    import torch
+
+    import hostlib
+    from strata_hip import _lib
+
+    _lib._lib = hostlib.load()
+
+    def stream_of(t):
+        if t.device.type != "cpu":
+            raise ValueError(f"tensor on {t.device}: the host build takes CPU tensors")
+        return None
+
+    _lib.stream_of = stream_of
+    torch.cuda.synchronize = lambda *a, **k: None
+    return torch.device("cpu")
 
 
 def rel_err(got, want) -> float:
