@@ -213,6 +213,11 @@ int sh_tile_glu(int kind, const void* gate, const void* up, const void* tables, 
 int sh_tile_down(int kind, const void* down, const void* tables, int64_t experts, int64_t rows, int64_t cols,
                  const void* h, int h_dtype, int64_t slots, const int32_t* tile_expert, const int32_t* pair,
                  int64_t pairs, void* out, void* stream);
+/* No counterpart in the reference (a tuning knob for callers and tests): whether the streamed tile products
+ * (sh_tile_matmul, sh_tile_glu of Q2_0 / IQ3_S) share the tiles of an expert's run of at most four tiles among
+ * several multiplying waves (on by default) or give each tile one wave. Both give the same bits. Returns the
+ * previous setting. Process-wide; not for use while another thread launches them. */
+int sh_tiles_set_share(int on);
 
 /* ---- dense layers: Q6_K held as three parts (strata_mlx/dense.py:109-167, ScaledLinear), w[r][c] = code[r][c] *
  * scale[r][c / 16] * d[r][c / d_step]: codes int8 (rows, cols), scales int8 (rows, cols / 16), d float16 (rows,

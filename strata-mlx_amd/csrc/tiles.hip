@@ -9,6 +9,7 @@
 // two buffers in turn, while the waves whose tiles are in the run multiply the previous chunk (16 pairs against RB
 // rows) on 16x16x32 MFMA, fp32 accumulators in registers, activation fragments straight from global memory. LDS
 // rows of a chunk are XOR-swizzled by 16-byte chunk so the MFMA operand reads fall in distinct banks.
+#include <atomic>
 #include <type_traits>
 
 #include "launch.h"
@@ -234,6 +235,7 @@ struct TileStreamArgs {
   int64_t n_src;               // TS_GLU: rows of x (tokens are clamped into them); TS_DOWN: output rows (pairs)
   int experts, rows, cols, rbytes, n_tiles;
   int tile0;                   // the first tile of this launch's window of at most TS_WT tiles
+  int share;                   // short units' tiles shared among consumer waves (sh_tiles_set_share)
 };
 
 template <int KIND> __host__ __device__ constexpr int ts_chunk_bytes() { return TS_KCH / wpb(KIND) * bpb(KIND); }
@@ -449,9 +451,17 @@ __global__ __launch_bounds__(TS_NT) void k_tile_stream(TileStreamArgs g) {
         if (cd.q < Q) dequant();  // cd.q == q + 1
       }
     } else {
-      // ---- consumers: the 64 rows (four fragments of 16) against tile cw of the unit; the fragments of
-      // chunk q in af[q & 1], loaded two steps ahead (the loop is unrolled by two: the buffers stay registers)
+      // ---- consumers: the 64 rows (four fragments of 16) against the unit's tiles. A unit of 5-8 tiles gives
+      // consumer cw tile cw and all four fragments; a shorter unit shares each tile among wpt waves (2 or 4: up to
+      // 8 waves busy), wave cw taking tile cw / wpt and fragments fg, fg + wpt, ... (fg = cw % wpt: for TS_GLU a
+      // gate fragment and the up fragment two on, so wpt <= 2). The activation fragments of the wave's tile for
+      // chunk q are in af[q & 1], loaded two steps ahead (the loop is unrolled by two: the buffers stay registers)
       const int cw = wave - 8;
+      auto wpt_of = [&](int len) {  // (TS_DOWN: one wave a tile; its registers are at the limit already)
+        constexpr int MAXW = MODE == TS_PLAIN ? 4 : MODE == TS_GLU ? 2 : 1;
+        return !g.share ? 1 : len <= 2 ? MAXW : len <= 4 ? min(2, MAXW) : 1;
+      };
+      auto tile_of = [&](int len) { return cw / wpt_of(len); };
       const XT* a = (const XT*)g.a;
       f32x4 acc[4];
       int pr[4] = {0, 0, 0, 0};  // TS_DOWN: the output rows of the lane's four slots in the current item
@@ -471,7 +481,8 @@ __global__ __launch_bounds__(TS_NT) void k_tile_stream(TileStreamArgs g) {
       };
       auto token_of = [&](const TsCursor& k) {
         int t = 0;
-        if (k.q < Q && cw < k.len) t = g.token[(int64_t)(k.start + cw) * TILE_TOKENS + (lane & 15)];
+        const int tl = tile_of(k.len);
+        if (k.q < Q && tl < k.len) t = g.token[(int64_t)(k.start + tl) * TILE_TOKENS + (lane & 15)];
         return t;
       };
       int tok_next = 0;
@@ -479,15 +490,16 @@ __global__ __launch_bounds__(TS_NT) void k_tile_stream(TileStreamArgs g) {
       auto load_a = [&](const TsCursor& s, auto bc) {  // chunk s.q's fragments of the lane's row into af[bc]
         constexpr int BUF = decltype(bc)::value;
         const int ln = opaque(lane), n = ln & 15, gq = ln >> 4;
+        const int tl = tile_of(s.len);
         if (s.c == 0) {  // a new item: the row of the lane's slot
-          int64_t row = (int64_t)(s.start + cw) * TILE_TOKENS + n;
+          int64_t row = (int64_t)(s.start + tl) * TILE_TOKENS + n;
           if constexpr (MODE == TS_GLU) {
             row = min(max((int64_t)tok_next, (int64_t)0), g.n_src - 1);
             tok_next = token_of(item_after(s));
           }
           arow = a + row * g.cols;
         }
-        if (cw < s.len) {
+        if (tl < s.len) {
           const int left = g.cols - s.c * TS_KCH;  // columns of the row from this chunk on
 #pragma unroll
           for (int ks = 0; ks < TS_KCH / 32; ++ks)
@@ -504,25 +516,30 @@ __global__ __launch_bounds__(TS_NT) void k_tile_stream(TileStreamArgs g) {
         const int q = s.q;
         lds_sync();
         const XT* wb = wl + (q & 1) * TS_BUF;
-        if (cw < s.len) {
+        // the wave's tile and fragments as constants of the path (a fragment count known at compile time keeps
+        // the accumulators and operands in registers)
+        auto multiply = [&](auto wc) {
+          constexpr int WPT = decltype(wc)::value, NF = 4 / WPT;
+          const int tl = cw / WPT, fg = cw - tl * WPT;
+          if (tl >= s.len) return;
           const int ln = opaque(lane), n = ln & 15, gq = ln >> 4;
           auto read_b = [&](int ks, u32x4* b) {
 #pragma unroll
-            for (int f = 0; f < 4; ++f) {
-              const int r = 16 * f + n;
-              b[f] = *(const u32x4*)(wb + r * TS_KCH + 8 * ((4 * ks + gq) ^ (r & 15)));
+            for (int j = 0; j < NF; ++j) {
+              const int r = 16 * (fg + WPT * j) + n;
+              b[j] = *(const u32x4*)(wb + r * TS_KCH + 8 * ((4 * ks + gq) ^ (r & 15)));
             }
           };
-          u32x4 b[2][4];  // the fragments of k-step ks + 1 are read while those of ks multiply
+          u32x4 b[2][NF];  // the fragments of k-step ks + 1 are read while those of ks multiply
           read_b(0, b[0]);
 #pragma unroll
           for (int ks = 0; ks < TS_KCH / 32; ++ks) {
             if (ks + 1 < TS_KCH / 32) read_b(ks + 1, b[(ks + 1) & 1]);
             __builtin_amdgcn_sched_barrier(0);  // (the scheduler would sink the reads to their MFMAs)
 #pragma unroll
-            for (int f = 0; f < 4; ++f) acc[f] = mfma<XT>(af[BUF][ks], b[ks & 1][f], acc[f]);
+            for (int j = 0; j < NF; ++j) acc[j] = mfma<XT>(af[BUF][ks], b[ks & 1][j], acc[j]);
           }
-          const int64_t slot0 = (int64_t)(s.start + cw) * TILE_TOKENS + 4 * gq;
+          const int64_t slot0 = (int64_t)(s.start + tl) * TILE_TOKENS + 4 * gq;
           if constexpr (MODE == TS_DOWN) {  // the slots' output rows, at the item's first chunk
             if (s.c == 0) {
 #pragma unroll
@@ -535,26 +552,37 @@ __global__ __launch_bounds__(TS_NT) void k_tile_stream(TileStreamArgs g) {
               if constexpr (MODE == TS_PLAIN) {
                 float* o = (float*)g.out + (slot0 + i) * g.rows + s.rb * VR + n;
 #pragma unroll
-                for (int f = 0; f < 4; ++f) o[16 * f] = acc[f][i];
-              } else if constexpr (MODE == TS_GLU) {
+                for (int j = 0; j < NF; ++j) o[16 * (fg + WPT * j)] = acc[j][i];
+              } else if constexpr (MODE == TS_GLU) {  // gate fragment j, its up fragment j + NF / 2
                 XT* o = (XT*)g.out + (slot0 + i) * g.rows + s.rb * VR + n;
 #pragma unroll
-                for (int f = 0; f < 2; ++f) {
-                  const float gt = acc[f][i], up = acc[f + 2][i];
-                  o[16 * f] = from_f32<XT>(gt / (1.0f + expf(-gt)) * up);
+                for (int j = 0; j < NF / 2; ++j) {
+                  const float gt = acc[j][i], up = acc[j + NF / 2][i];
+                  o[16 * (fg + WPT * j)] = from_f32<XT>(gt / (1.0f + expf(-gt)) * up);
                 }
               } else {
                 const int p = pr[i];
                 if (p >= 0 && p < g.n_src) {
                   XT* o = (XT*)g.out + (int64_t)p * g.rows + s.rb * VR + n;
 #pragma unroll
-                  for (int f = 0; f < 4; ++f) o[16 * f] = from_f32<XT>(acc[f][i]);
+                  for (int j = 0; j < NF; ++j) o[16 * (fg + WPT * j)] = from_f32<XT>(acc[j][i]);
                 }
               }
             }
 #pragma unroll
             for (int f = 0; f < 4; ++f) acc[f] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
           }
+        };
+        if constexpr (MODE == TS_DOWN) {
+          multiply(std::integral_constant<int, 1>{});
+        } else {
+          const int wpt = wpt_of(s.len);
+          if (wpt == 1)
+            multiply(std::integral_constant<int, 1>{});
+          else if (MODE == TS_GLU || wpt == 2)
+            multiply(std::integral_constant<int, 2>{});
+          else
+            multiply(std::integral_constant<int, (MODE == TS_GLU ? 2 : 4)>{});
         }
         __builtin_amdgcn_sched_barrier(0);  // chunk q + 2's fragments load after chunk q's are consumed
         cur_next(cs);
@@ -586,6 +614,10 @@ __global__ __launch_bounds__(TS_NT) void k_tile_stream(TileStreamArgs g) {
   }
 }
 
+// whether the stream kernels share a short unit's tiles among consumer waves (on unless switched off, for
+// measuring the two forms against each other)
+static std::atomic<int> g_share{1};
+
 template <int KIND, typename XT, int MODE>
 static int launch_stream(const TileStreamArgs& g, hipStream_t stream, const char* what) {
   constexpr size_t lds = ts_lds_bytes<KIND, XT>();
@@ -596,6 +628,7 @@ static int launch_stream(const TileStreamArgs& g, hipStream_t stream, const char
   for (int w0 = 0; w0 < g.n_tiles; w0 += TS_WT) {
     TileStreamArgs gw = g;
     gw.tile0 = w0;
+    gw.share = g_share.load(std::memory_order_relaxed);
     hipLaunchKernelGGL(kern, dim3((unsigned)device_cus()), dim3(TS_NT), lds, stream, gw);
     const int st = check_launch(what);
     if (st) return st;
@@ -682,6 +715,8 @@ int sh_tile_glu(int kind, const void* gate, const void* up, const void* tables, 
                          : launch_stream<Q2_0, XT, TS_GLU>(g, (hipStream_t)stream, "tile_glu");
   });
 }
+
+int sh_tiles_set_share(int on) { return g_share.exchange(on ? 1 : 0); }
 
 int sh_tile_down(int kind, const void* down, const void* tables, int64_t experts, int64_t rows, int64_t cols,
                  const void* h, int h_dtype, int64_t slots, const int32_t* tile_expert, const int32_t* pair,

@@ -50,6 +50,7 @@ PROTOTYPES = {
                             c_vp, c_int, c_i64, c_i64, c_i64, c_i64, c_vp, c_vp, c_sz, c_vp],
     "sh_moe_set_tail_combine": [c_int],
     "sh_moe_set_one_launch": [c_int],
+    "sh_tiles_set_share": [c_int],
     "sh_moe_scratch_bytes": [],
     "sh_moe_decode_noalloc": [c_int, c_int, c_vp, c_vp, c_vp, c_i64, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_int, c_vp,
                               c_int, c_i64, c_i64, c_i64, c_i64, c_vp, c_vp, c_vp, c_vp],

@@ -23,8 +23,9 @@ from concurrent.futures import ThreadPoolExecutor
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(os.path.dirname(HERE))
-CSRC = os.path.join(ROOT, "strata-mlx_amd", "csrc")
-OUT = os.path.join(HERE, "_out")
+# HOSTRUN_CSRC / HOSTRUN_OUT: another tree's sources into another output (two versions of a kernel side by side)
+CSRC = os.environ.get("HOSTRUN_CSRC", os.path.join(ROOT, "strata-mlx_amd", "csrc"))
+OUT = os.environ.get("HOSTRUN_OUT", os.path.join(HERE, "_out"))
 CXX = os.environ.get("HOSTRUN_CXX", "/opt/rocm/llvm/bin/clang++")
 
 
@@ -155,6 +156,16 @@ def rewrite(text: str) -> str:
 
 
 def build(asan: bool = False, verbose: bool = True) -> str:
+    """The library, rebuilt when its sources changed; one build at a time across processes (a lock file)."""
+    import fcntl
+
+    os.makedirs(OUT, exist_ok=True)
+    with open(os.path.join(OUT, ".lock"), "w") as lock:
+        fcntl.flock(lock, fcntl.LOCK_EX)
+        return _build(asan, verbose)
+
+
+def _build(asan: bool, verbose: bool) -> str:
     lib = library_path(asan)
     stamp = lib + ".hash"
     h = source_hash()
@@ -176,7 +187,7 @@ def build(asan: bool = False, verbose: bool = True) -> str:
         if not name.endswith(".h"):
             units.append(dst)
     units.append(os.path.join(HERE, "hostrun.cpp"))
-    flags = ["-std=c++17", "-O1", "-fPIC", "-g0", "-w", "-x", "c++", "-I", HERE, "-I", src_dir,
+    flags = ["-std=c++17", "-O2", "-fPIC", "-g0", "-w", "-x", "c++", "-I", HERE, "-I", src_dir,
              "-fno-strict-aliasing"]
     if asan:
         flags += ["-fsanitize=address", "-fno-omit-frame-pointer"]

@@ -141,35 +141,45 @@ struct F4 {
   float v[4];
 };
 
+inline float hostrun_half(uint16_t h, bool bf) {
+  if (bf) {
+    const uint32_t u = (uint32_t)h << 16;
+    float f;
+    memcpy(&f, &u, 4);
+    return f;
+  }
+  _Float16 v;
+  memcpy(&v, &h, 2);
+  return (float)v;
+}
+
 // D = C + A B for one 16 x 16 tile of a wave, K = 4 KPL: lane l holds A[l % 16][k] and B[k][l % 16] for
-// k = KPL (l / 16) .. + KPL - 1, and D[4 (l / 16) + r][l % 16], r = 0..3
+// k = KPL (l / 16) .. + KPL - 1, and D[4 (l / 16) + r][l % 16], r = 0..3. The products of 16-bit values are exact
+// in float32; the sums here are float32 in k order (the hardware's order and roundings of its sums differ at the
+// last bits).
 template <int KPL, bool BF> inline F4 mfma(const MfmaIn<KPL>& in) {
   return wave_op<MfmaIn<KPL>, F4>(in, [](const MfmaIn<KPL>* x, F4* d, uint64_t live) {
     if (live != ~0ull) die("an MFMA with lanes that have returned");
-    auto el = [](const unsigned char* p, int j) -> double {
-      uint16_t h;
-      memcpy(&h, p + 2 * j, 2);
-      if (BF) {
-        uint32_t u = (uint32_t)h << 16;
-        float f;
-        memcpy(&f, &u, 4);
-        return f;
-      }
-      _Float16 v;
-      memcpy(&v, &h, 2);
-      return (float)v;
-    };
+    constexpr int K = 4 * KPL;
+    float A[16][K], B[16][K], C[16][16];  // B by column
     for (int l = 0; l < 64; ++l) {
-      const int n = l % 16;
-      for (int r = 0; r < 4; ++r) {
-        const int m = 4 * (l / 16) + r;
-        double s = 0.0;
-        for (int g = 0; g < 4; ++g)
-          for (int j = 0; j < KPL; ++j) s += el(x[m + 16 * g].a, j) * el(x[n + 16 * g].b, j);
-        // the C operand of row m, column n sits in lane n + 16 (m / 4), element m % 4
-        d[l].v[r] = (float)((double)x[n + 16 * (m / 4)].c[m % 4] + s);
+      uint16_t ha[KPL], hb[KPL];
+      memcpy(ha, x[l].a, sizeof ha);
+      memcpy(hb, x[l].b, sizeof hb);
+      for (int j = 0; j < KPL; ++j) {
+        A[l % 16][KPL * (l / 16) + j] = hostrun_half(ha[j], BF);
+        B[l % 16][KPL * (l / 16) + j] = hostrun_half(hb[j], BF);
       }
+      for (int r = 0; r < 4; ++r) C[4 * (l / 16) + r][l % 16] = x[l].c[r];
     }
+    for (int m = 0; m < 16; ++m)
+      for (int n = 0; n < 16; ++n) {
+        float s = 0.0f;
+        for (int k = 0; k < K; ++k) s = fmaf(A[m][k], B[n][k], s);
+        C[m][n] += s;
+      }
+    for (int l = 0; l < 64; ++l)
+      for (int r = 0; r < 4; ++r) d[l].v[r] = C[4 * (l / 16) + r][l % 16];
   });
 }
 

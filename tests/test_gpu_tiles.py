@@ -181,3 +181,41 @@ def test_a_float32_prompt_through_the_tiles(tables, dev):
     assert got.shape == (T, K, D) and got.dtype == torch.float32
     want, _ = prompt_want(ws["g"], ws["u"], ws["d"], x, idx, "float32")
     assert np.abs(got.cpu().numpy().reshape(-1, D) - want).max() <= 1e-4 * np.abs(want).max()
+
+
+@pytest.mark.parametrize("kind, dtype", [("IQ3_S", torch.bfloat16), ("Q2_0", torch.float16)])
+def test_shared_tiles_give_one_wave_a_tiles_bits(kind, dtype, tables, dev):
+    """Experts' runs of 1-8 tiles (Zipf routing over few experts): the streamed products with a short run's tiles
+    shared among waves (each wave some of the 64 rows) give the bits of one wave a tile, for tile_matmul and for
+    the fused gate / up + SwiGLU, call after call."""
+    from strata_hip import _lib
+
+    E, F, D, T, K = 24, 256, 512, 96, 6
+    rng = np.random.default_rng(12)
+    raws = {n: torch.from_numpy(synth.random_blocks(kind, E * r, c, rng)).to(dev)
+            for n, (r, c) in (("g", (F, D)), ("u", (F, D)), ("d", (D, F)))}
+    lin = {n: SB.BlockSwitchLinear(raws[n], kind, (E, F, D) if n != "d" else (E, D, F)) for n in raws}
+    idx = torch.from_numpy(OR.top_k(synth.zipf_logits(rng, T, E).float().numpy(), K)).to(dev)
+    x = torch.from_numpy(rng.standard_normal((T, D)).astype(np.float32)).to(dtype).to(dev)
+    te, token, where = SB.tiles_of(idx, E)
+    runs = torch.bincount(te[te < E].long(), minlength=E)
+    assert runs.max() >= 5 and (runs[runs > 0] <= 4).any()  # long and short runs both
+    a = x[token.long()]
+    valid = (te < E).repeat_interleave(16)
+    lib = _lib.load()
+    before = lib.sh_tiles_set_share(1)
+    try:
+        shared = (SB.tile_matmul(raws["g"], kind, (E, F, D), a, te)[valid],
+                  SB.tile_glu(lin["g"], lin["u"], x, token, te)[valid])
+        torch.cuda.synchronize()
+        lib.sh_tiles_set_share(0)
+        alone = (SB.tile_matmul(raws["g"], kind, (E, F, D), a, te)[valid],
+                 SB.tile_glu(lin["g"], lin["u"], x, token, te)[valid])
+        torch.cuda.synchronize()
+        lib.sh_tiles_set_share(1)
+        again = SB.tile_glu(lin["g"], lin["u"], x, token, te)[valid]
+    finally:
+        lib.sh_tiles_set_share(before)
+    assert torch.equal(shared[0], alone[0])
+    assert torch.equal(shared[1].view(torch.int16), alone[1].view(torch.int16))
+    assert torch.equal(again.view(torch.int16), shared[1].view(torch.int16))
