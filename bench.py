@@ -385,72 +385,127 @@ def prefill_layer(dev, steps, warmup):
     return res
 
 
-def cpu_baseline(raw, inputs, kind, seconds, check_outputs, threads=1):
+_CPU = {}  # a worker's view of the sampled layers' blocks (mapped files), set by _cpu_attach
+
+
+def _cpu_attach(names, kind):
+    """Pool initializer: map the parent's file copies of the sampled layers' routed stacks (read-only)."""
+    import numpy as np
+    from threadpoolctl import threadpool_limits
+
+    _CPU["limits"] = threadpool_limits(limits=1)  # one BLAS thread a worker
+    _CPU["kind"] = kind
+    _CPU["layers"] = [[np.memmap(path, dtype=np.uint8, mode="r", shape=shape) for path, shape in layer]
+                      for layer in names]
+
+
+def _cpu_expert(l, e, xs):
+    """One routed expert of a sampled layer for the token rows xs (n, D): its down(swiglu(gate, up)) rows, as the
+    reference's CPU path computes them (the expert dequantized, float32 products, bfloat16 roundings)."""
+    from oracle import blocks as OB
+    from oracle import route as OR
+
+    g, u, d = _CPU["layers"][l][:3]
+    kind = _CPU["kind"]
+    mg, mu, md = (OB.dequantize(m[e], kind, shape, {}) for m, shape in ((g, (F, D)), (u, (F, D)), (d, (D, F))))
+    h = OR.swiglu(OR.to_bf16(xs @ mg.T), OR.to_bf16(xs @ mu.T), "bfloat16")
+    return OR.to_bf16(h @ md.T)
+
+
+def _expert_products(xs, mats, kind):
+    from oracle import blocks as OB
+    from oracle import route as OR
+
+    mg, mu, md = (OB.dequantize(m, kind, shape, {}) for m, shape in zip(mats, ((F, D), (F, D), (D, F))))
+    h = OR.swiglu(OR.to_bf16(xs @ mg.T), OR.to_bf16(xs @ mu.T), "bfloat16")
+    return OR.to_bf16(h @ md.T)
+
+
+def cpu_baseline(raw, inputs, kind, seconds, check_outputs, procs=1, max_layers=9):
     """The oracle's restatement of the reference's CPU path (dequantize the touched experts, numpy matmul in
-    float32, the reference's routing, SwiGLU and combine roundings) on the host cores: one thread, or `threads`
-    (the touched experts dequantized and multiplied on a pool of that many threads, each product on one BLAS
-    thread: the parallelism is over experts)."""
-    from concurrent.futures import ThreadPoolExecutor
+    float32, the reference's routing, SwiGLU and combine roundings) on the host cores, over the first `max_layers`
+    layers: in this process (procs = 1, one BLAS thread), or spread over `procs` worker processes, an expert a task
+    (each worker one BLAS thread, the layers' routed stacks in files it maps). Returns GB/s of algorithmic bytes, the
+    seconds spent, the layer decodes done, the layers used and the check against the GPU's outputs."""
+    import multiprocessing as mp
+    import shutil
+    import tempfile
 
     import numpy as np
     from threadpoolctl import threadpool_limits
 
-    from oracle import blocks as OB
     from oracle import route as OR
 
-    pool = ThreadPoolExecutor(threads) if threads > 1 else None
+    n_layers = min(len(raw), max_layers)
+    host, names = [], []
+    tmp = None
+    if procs > 1:  # in memory (/dev/shm) when it has room for them twice over, else in the temporary directory
+        need = sum(raw[l][i].numel() for l in range(n_layers) for i in range(3))
+        shm_ok = os.path.isdir("/dev/shm") and shutil.disk_usage("/dev/shm").free > 2 * need
+        tmp = tempfile.mkdtemp(prefix="cpu_baseline_", dir="/dev/shm" if shm_ok else None)
+    for l in range(n_layers):
+        mats, layer_names = [], []
+        for i, (t, n) in enumerate(zip(raw[l][:6], (E, E, E, 1, 1, 1))):
+            a = t.cpu().numpy().reshape(n, -1)
+            if tmp and n == E:  # the routed stacks, as files the workers map
+                path = os.path.join(tmp, f"{l}_{i}")
+                m = np.memmap(path, dtype=np.uint8, mode="w+", shape=a.shape)
+                m[:] = a
+                m.flush()
+                layer_names.append((path, a.shape))
+            mats.append(a)
+        mats.append(raw[l][6].float().cpu().numpy())
+        host.append(mats)
+        names.append(layer_names)
+    pool = None
+    if procs > 1:
+        pool = mp.get_context("spawn").Pool(procs, initializer=_cpu_attach, initargs=(names, kind))
+        pool.starmap(_cpu_expert, [(0, 0, np.zeros((1, D), np.float32))] * procs)  # workers up before the clock
 
-    def one_layer(lw, logits, x):
-        g, u, d, sg, su, sd, wg = lw
+    def one_layer(l, logits, x):
+        g, u, d, sg, su, sd, wg = host[l]
         idx = OR.top_k(logits, K)
         w = OR.routing_weights(logits, idx)
         B = x.shape[0]
         ys = np.zeros((B, K, D), np.float32)
-
-        def expert(e):
-            mats = [OB.dequantize(m[int(e)], kind, shape, {}) for m, shape in ((g, (F, D)), (u, (F, D)), (d, (D, F)))]
-            for t, j in zip(*np.nonzero(idx == e)):
-                h = OR.swiglu(OR.to_bf16(mats[0] @ x[t]), OR.to_bf16(mats[1] @ x[t]), "bfloat16")
-                ys[t, j] = OR.to_bf16(mats[2] @ h)
-
         used = np.unique(idx)
+        tasks = [(int(e), np.nonzero(idx == e)) for e in used]
         if pool is None:
-            for e in used:
-                expert(e)
+            outs = [_expert_products(x[t], (g[e], u[e], d[e]), kind) for e, (t, _) in tasks]
         else:
-            list(pool.map(expert, used))
-        shw = [OB.dequantize(m[0], kind, shape, {}) for m, shape in ((sg, (F, D)), (su, (F, D)), (sd, (D, F)))]
-        s = np.stack([OR.to_bf16(shw[2] @ OR.swiglu(OR.to_bf16(shw[0] @ x[t]), OR.to_bf16(shw[1] @ x[t]), "bfloat16"))
-                      for t in range(B)])
+            outs = pool.starmap(_cpu_expert, [(l, e, x[t]) for e, (t, _) in tasks])
+        for (e, (t, j)), y in zip(tasks, outs):
+            ys[t, j] = y
+        s = _expert_products(x, (sg[0], su[0], sd[0]), kind)
         gate = OR.to_bf16(x @ wg)
         return OR.moe_combine(ys, w, gate, s, "bfloat16"), len(used)
 
-    host = {}
     total_bytes, total_time, layers_done, checks = 0, 0.0, 0, {}
-    with threadpool_limits(limits=1):
-        b_list = sorted(inputs)
-        l = 0
-        while True:
-            for b in b_list:
-                logits_t, x_t, gpu_out = inputs[b][l % len(inputs[b])]
-                if l not in host:
-                    g, u, d, sg, su, sd, wg = raw[l % len(raw)]
-                    host[l] = tuple(t.cpu().numpy().reshape(n, -1) for t, n in
-                                    ((g, E), (u, E), (d, E), (sg, 1), (su, 1), (sd, 1))) + (wg.float().cpu().numpy(),)
-                logits, x = logits_t.float().cpu().numpy(), x_t.float().cpu().numpy()
-                t0 = time.perf_counter()
-                out, n_unique = one_layer(host[l], logits, x)
-                total_time += time.perf_counter() - t0
-                total_bytes += layer_bytes(n_unique, b)
-                layers_done += 1
-                if check_outputs and l == 0 and gpu_out is not None:
-                    got = gpu_out.float().cpu().numpy()
-                    checks[b] = float(np.abs(got - out).max() / max(np.abs(out).max(), 1e-30))
-            l += 1
-            if total_time >= seconds or l >= len(raw):
-                break
-    if pool is not None:
-        pool.shutdown()
+    try:
+        with threadpool_limits(limits=1):
+            b_list = sorted(inputs)
+            l = 0
+            while True:
+                for b in b_list:
+                    logits_t, x_t, gpu_out = inputs[b][l % len(inputs[b])]
+                    logits, x = logits_t.float().cpu().numpy(), x_t.float().cpu().numpy()
+                    t0 = time.perf_counter()
+                    out, n_unique = one_layer(l, logits, x)
+                    total_time += time.perf_counter() - t0
+                    total_bytes += layer_bytes(n_unique, b)
+                    layers_done += 1
+                    if check_outputs and l == 0 and gpu_out is not None:
+                        got = gpu_out.float().cpu().numpy()
+                        checks[b] = float(np.abs(got - out).max() / max(np.abs(out).max(), 1e-30))
+                l += 1
+                if total_time >= seconds or l >= n_layers:
+                    break
+    finally:
+        if pool is not None:
+            pool.close()
+            pool.join()
+        if tmp:
+            shutil.rmtree(tmp, ignore_errors=True)
     return total_bytes / total_time / 1e9, total_time, layers_done, l, checks
 
 
@@ -593,10 +648,12 @@ def main():
         for threads in (1, cores):
             gbs, secs, n_done, n_layers_used, checks = cpu_baseline(raw, inputs, args.kind, args.cpu_seconds,
                                                                     threads == 1, threads)
+            how = ("one process" if threads == 1 else
+                   f"{threads} worker processes, an expert a task, the blocks in mapped files")
             legs[threads] = {"value": round(gbs, 4), "unit": "GB/s", "cores": threads, "kind": "port",
                              "sample": f"{n_done} layer decodes (layers 0..{n_layers_used - 1} at B = {args.batches}), "
                                        f"{secs:.1f} s: numpy dequantize of the touched experts + float32 matmul, "
-                                       f"{threads} thread(s) over the experts, one BLAS thread each"}
+                                       f"{how}, one BLAS thread each"}
             if checks:
                 legs[threads]["check_vs_gpu_rel_err"] = {str(k): round(v, 6) for k, v in checks.items()}
             print(f"# CPU {threads} thread(s): {legs[threads]}", file=sys.stderr, flush=True)
