@@ -183,7 +183,33 @@ void load_lds(const void* src, uint32_t m0) {
   memcpy(L.lds + at, src, 16);
 }
 
+// HOSTRUN_SEED=<n>: the workgroups of a launch in a shuffled order, and in every scheduling pass the waves of a
+// workgroup in a shuffled order (a wave's lanes stay in order): a kernel whose waves share LDS without a barrier
+// between the write and the read, or whose result depends on which workgroup finishes last, gives different
+// results from seed to seed
+struct Shuffle {
+  uint64_t state = 0;
+  bool on = false;
+  Shuffle() {
+    if (const char* e = getenv("HOSTRUN_SEED")) {
+      on = true;
+      state = 0x9e3779b97f4a7c15ull ^ strtoull(e, nullptr, 10);
+    }
+  }
+  uint64_t next() {  // xorshift64*
+    state ^= state >> 12;
+    state ^= state << 25;
+    state ^= state >> 27;
+    return state * 0x2545f4914f6cdd1dull;
+  }
+  template <class V> void apply(V& v) {
+    if (!on) return;
+    for (size_t i = v.size(); i > 1; --i) std::swap(v[i - 1], v[next() % i]);
+  }
+};
+
 void launch(const char* name, dim3 grid, dim3 block, size_t shmem, const std::function<void()>& body) {
+  static Shuffle shuffle;
   const size_t n = (size_t)block.x * block.y * block.z;
   if (n == 0 || n > 1024) die("a workgroup of %zu threads", n);
   if ((size_t)grid.x * grid.y * grid.z == 0) die("an empty grid");
@@ -197,10 +223,17 @@ void launch(const char* name, dim3 grid, dim3 block, size_t shmem, const std::fu
   L.lds_bytes = shmem;
   block_dim = Idx3{block.x, block.y, block.z};
   grid_dim = Idx3{grid.x, grid.y, grid.z};
+  std::vector<Idx3> order;
+  order.reserve((size_t)grid.x * grid.y * grid.z);
   for (uint32_t bz = 0; bz < grid.z; ++bz)
     for (uint32_t by = 0; by < grid.y; ++by)
-      for (uint32_t bx = 0; bx < grid.x; ++bx) {
-        block_idx = Idx3{bx, by, bz};
+      for (uint32_t bx = 0; bx < grid.x; ++bx) order.push_back(Idx3{bx, by, bz});
+  shuffle.apply(order);
+  const size_t n_waves = (n + 63) / 64;
+  std::vector<size_t> wave_order(n_waves);
+  for (size_t w = 0; w < n_waves; ++w) wave_order[w] = w;
+  for (const Idx3& b : order) {
+        block_idx = b;
         memset(L.lds, 0xa5, shmem);  // what the previous workgroup left: nothing to rely on
         for (Wave& w : L.waves) {
           w.live = w.arrived = 0;
@@ -219,13 +252,15 @@ void launch(const char* name, dim3 grid, dim3 block, size_t shmem, const std::fu
         L.at_barrier = 0;
         for (;;) {
           bool ran = false;
-          for (size_t i = 0; i < n; ++i) {
-            Fiber& f = L.fibers[i];
-            if (f.state != READY) continue;
-            cur = &f;
-            hostrun_switch(&L.sched_sp, f.sp);
-            ran = true;
-          }
+          shuffle.apply(wave_order);
+          for (size_t w : wave_order)
+            for (size_t i = w * 64; i < std::min(n, w * 64 + 64); ++i) {
+              Fiber& f = L.fibers[i];
+              if (f.state != READY) continue;
+              cur = &f;
+              hostrun_switch(&L.sched_sp, f.sp);
+              ran = true;
+            }
           if (L.live == 0) break;
           if (!ran) deadlock();
         }
