@@ -69,6 +69,12 @@ def _on_gpu(*ts):
     return dev
 
 
+def _check_stack(blocks: torch.Tensor, kind: str, n: int, rows: int, cols: int, what: str) -> None:
+    """The bytes a kernel reads for n (rows, cols) matrices of `kind` are all in `blocks` (the C ABI cannot know)."""
+    if blocks.numel() < n * rows * row_bytes(kind, cols):
+        raise ValueError(f"{what}: {blocks.numel()} bytes for {n} x ({rows}, {cols}) {kind} weights")
+
+
 def _u8(blocks: torch.Tensor) -> torch.Tensor:
     if blocks.dtype != torch.uint8 or not blocks.is_contiguous():
         raise ValueError("blocks: a contiguous uint8 tensor of the file's bytes expected")
@@ -100,6 +106,8 @@ def switch_matvec(blocks: torch.Tensor, kind: str, shape: tuple, idx: torch.Tens
     """out[pair] = W[idx[pair]] . x[pair // share] for a stack of `shape` (experts, rows, cols); (pairs, rows)
     in x's type. The kernel behind BlockSwitchLinear (strata_mlx/blocks.py:196-220, 420-436)."""
     experts, rows, cols = shape
+    _check_cols(kind, cols)
+    _check_stack(blocks, kind, experts, rows, cols, "switch_matvec")
     idx = _idx32(idx)
     pairs = idx.numel()
     x = x.reshape(-1, cols).contiguous()
@@ -168,6 +176,8 @@ def window_matvec(blocks: torch.Tensor, kind: str, rows: int, cols: int, x: torc
     """out[t] = W . x[t] for one layer `blocks` of (rows, cols) and x (tokens, cols). Returns (tokens, rows)
     (strata_mlx/blocks.py:384-394). `per_row` is accepted for the interface; the library chooses its lanes. A token's
     bits do not depend on the window it is in, on either path."""
+    _check_cols(kind, cols)
+    _check_stack(blocks, kind, 1, rows, cols, "window_matvec")
     x = x.reshape(-1, cols).contiguous()
     tokens = x.shape[0]
     if stack_takes(kind, cols, x.dtype) and 0 < tokens <= 16:
@@ -376,6 +386,7 @@ def tile_matmul(blocks: torch.Tensor, kind: str, shape: tuple, a: torch.Tensor, 
     experts, rows, cols = shape
     if not tileable(kind, rows, cols):
         raise ValueError(f"tile_matmul: {kind} ({rows}, {cols}) is not tileable")
+    _check_stack(blocks, kind, experts, rows, cols, "tile_matmul")
     a = a.contiguous()
     p = a.shape[0]
     if p % TOKENS_TILE or a.shape[1] != cols:

@@ -69,3 +69,26 @@ def test_window_linear_answers_like_the_references():
     x = torch.ones(1, 9, 16, dtype=torch.float16)
     lin.weight.data.fill_(0.5)
     assert torch.equal(wl(x), lin(x))  # (on the CPU the layer's own product)
+
+
+def test_block_buffers_too_small_are_refused_before_any_launch():
+    """The C ABI takes bare pointers: the Python layer checks that every byte a kernel reads lies in the tensor it
+    passes (a short buffer would be read past its end on the GPU)."""
+    import pytest
+
+    E, R, C = 4, 64, 512
+    whole = torch.zeros(E * R * SB.row_bytes("Q2_0", C), dtype=torch.uint8)
+    short = whole[:-18]  # one Q2_0 block short
+    x = torch.zeros((8, C), dtype=torch.bfloat16)
+    idx = torch.zeros(8, dtype=torch.int32)
+    with pytest.raises(ValueError, match="bytes for"):
+        SB.switch_matvec(short, "Q2_0", (E, R, C), idx, x, 1)
+    with pytest.raises(ValueError, match="bytes for"):
+        SB.window_matvec(short[: R * SB.row_bytes("Q2_0", C) - 18], "Q2_0", R, C, x)
+    with pytest.raises(ValueError, match="bytes for"):
+        SB.tile_matmul(short, "Q2_0", (E, R, C), torch.zeros((16, C), dtype=torch.bfloat16),
+                       torch.zeros(1, dtype=torch.int32))
+    with pytest.raises(ValueError, match="bytes for"):
+        SB.stack_matvec(short, "Q2_0", (E, R, C), torch.zeros((E, 1, C), dtype=torch.bfloat16))
+    with pytest.raises(ValueError, match="bytes for"):
+        SB.BlockSwitchLinear(short, "Q2_0", (E, R, C))
