@@ -335,7 +335,8 @@ def prefill_layer(dev, steps, warmup):
     three grouped GEMMs on MFMA with the weights dequantized into LDS as bf16 (gate and up with the SwiGLU in one
     pass, down with the un-permutation in another). Timed: tiles_of + both passes, as one captured graph (the
     layer's whole prompt path after routing). MFMA use = 2 * pairs * (3 * 512 * 2048) flops / time against the
-    2.5 PFLOP/s dense bf16 peak."""
+    2.5 PFLOP/s dense bf16 peak. us_one_wave_a_tile: the same with each tile multiplied by one wave
+    (sh_tiles_set_share(0)), the form before short expert runs were shared."""
     import numpy as np
     import torch
 
@@ -357,29 +358,43 @@ def prefill_layer(dev, steps, warmup):
     def layer():
         return SB._tiled_glu(x[None], idx[None], up, gate, down)
 
-    stream = torch.cuda.Stream()
-    stream.wait_stream(torch.cuda.current_stream())
-    with torch.cuda.stream(stream):
-        layer()
-        torch.cuda.synchronize()
-        graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(graph, stream=stream):
-            layer()
-        for _ in range(warmup):
-            graph.replay()
-        torch.cuda.synchronize()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record(stream)
-        for _ in range(steps):
-            graph.replay()
-        e1.record(stream)
-        torch.cuda.synchronize()
-    sec = e0.elapsed_time(e1) * 1e-3 / steps
+    from strata_hip import _lib
+
+    lib = _lib.load()
+
+    def timed(share):
+        """The layer as a graph captured with the stream kernels' tile sharing on or off (read at launch)."""
+        before = lib.sh_tiles_set_share(share)
+        try:
+            stream = torch.cuda.Stream()
+            stream.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(stream):
+                layer()
+                torch.cuda.synchronize()
+                graph = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(graph, stream=stream):
+                    layer()
+                for _ in range(warmup):
+                    graph.replay()
+                torch.cuda.synchronize()
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                e0.record(stream)
+                for _ in range(steps):
+                    graph.replay()
+                e1.record(stream)
+                torch.cuda.synchronize()
+        finally:
+            lib.sh_tiles_set_share(before)
+        return e0.elapsed_time(e1) * 1e-3 / steps
+
+    sec = timed(1)
+    sec_alone = timed(0)
     flops = 2 * pairs * 3 * F_ * D_
     counts = torch.bincount(idx.reshape(-1).long(), minlength=E_)
     tiles = int(((counts + 15) // 16).sum())
     res = {"us": round(sec * 1e6, 1), "TFLOPs": round(flops / sec / 1e12, 1),
-           "mfma_frac": round(flops / sec / 2.5e15, 4), "pairs": pairs, "tiles": tiles,
+           "mfma_frac": round(flops / sec / 2.5e15, 4), "us_one_wave_a_tile": round(sec_alone * 1e6, 1),
+           "pairs": pairs, "tiles": tiles,
            "top_expert_pairs": int(counts.max()), "experts_used": int((counts > 0).sum())}
     print(f"# C5 prefill: {res}", file=sys.stderr, flush=True)
     return res
