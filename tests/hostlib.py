@@ -24,13 +24,15 @@ class HostError(RuntimeError):
 
 def load(asan: bool | None = None) -> ctypes.CDLL:
     """The host build (built first if the sources changed), with the package's prototypes. With HOSTRUN_ASAN=1 in
-    the environment the AddressSanitizer build (the process must preload the sanitizer's runtime)."""
+    the environment the AddressSanitizer build (the process must preload the sanitizer's runtime); with HOSTRUN_COV=1 the
+    line-coverage build."""
     if asan is None:
         asan = os.environ.get("HOSTRUN_ASAN") == "1"
+    cov = os.environ.get("HOSTRUN_COV") == "1"
     if asan not in _libs:
         from strata_hip import _lib as L
 
-        lib = ctypes.CDLL(_build.build(asan=asan, verbose=False))
+        lib = ctypes.CDLL(_build.build(asan=asan, verbose=False, cov=cov))
         for name, args in L.PROTOTYPES.items():
             fn = getattr(lib, name, None)
             if fn is None:

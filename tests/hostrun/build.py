@@ -1,7 +1,7 @@
 """Compile the library's HIP sources for the host (test infrastructure: the CPU tests run the kernels themselves with
 it; the package never loads it).
 
-    python tests/hostrun/build.py [--asan]
+    python tests/hostrun/build.py [--asan] [--cov]
 
 The sources in strata-mlx_amd/csrc are copied to tests/hostrun/_out/src with four mechanical rewrites the host
 compiler needs, and compiled as C++ against hip/hip_runtime.h of this directory (the device environment restated
@@ -29,8 +29,8 @@ OUT = os.environ.get("HOSTRUN_OUT", os.path.join(HERE, "_out"))
 CXX = os.environ.get("HOSTRUN_CXX", "/opt/rocm/llvm/bin/clang++")
 
 
-def library_path(asan: bool = False) -> str:
-    return os.path.join(OUT, "libstrata_host_asan.so" if asan else "libstrata_host.so")
+def library_path(asan: bool = False, cov: bool = False) -> str:
+    return os.path.join(OUT, "libstrata_host" + ("_asan" if asan else "") + ("_cov" if cov else "") + ".so")
 
 
 def _inputs():
@@ -149,30 +149,32 @@ def rewrite(text: str) -> str:
             continue
         end = _close(text, m.end() - 1)
         out.append(text[i:m.start()])
-        out.append(_asm(text[m.start():end]))
+        stmt = text[m.start():end]
+        out.append(_asm(stmt) + "\n" * stmt.count("\n"))  # (line numbers kept: coverage and messages)
         i = end
     out.append(text[i:])
     return "".join(out)
 
 
-def build(asan: bool = False, verbose: bool = True) -> str:
-    """The library, rebuilt when its sources changed; one build at a time across processes (a lock file)."""
+def build(asan: bool = False, verbose: bool = True, cov: bool = False) -> str:
+    """The library, rebuilt when its sources changed; one build at a time across processes (a lock file). cov: line
+    coverage (gcov's notes and counts beside the objects in _out/obj_cov)."""
     import fcntl
 
     os.makedirs(OUT, exist_ok=True)
     with open(os.path.join(OUT, ".lock"), "w") as lock:
         fcntl.flock(lock, fcntl.LOCK_EX)
-        return _build(asan, verbose)
+        return _build(asan, verbose, cov)
 
 
-def _build(asan: bool, verbose: bool) -> str:
-    lib = library_path(asan)
+def _build(asan: bool, verbose: bool, cov: bool = False) -> str:
+    lib = library_path(asan, cov)
     stamp = lib + ".hash"
     h = source_hash()
     if os.path.exists(lib) and os.path.exists(stamp) and open(stamp).read().strip() == h:
         return lib
     src_dir = os.path.join(OUT, "src")
-    obj_dir = os.path.join(OUT, "obj_asan" if asan else "obj")
+    obj_dir = os.path.join(OUT, "obj" + ("_asan" if asan else "") + ("_cov" if cov else ""))
     os.makedirs(src_dir, exist_ok=True)
     os.makedirs(obj_dir, exist_ok=True)
     srcs, _ = _inputs()
@@ -191,6 +193,8 @@ def _build(asan: bool, verbose: bool) -> str:
              "-fno-strict-aliasing"]
     if asan:
         flags += ["-fsanitize=address", "-fno-omit-frame-pointer"]
+    if cov:
+        flags += ["--coverage"]
 
     def compile_one(src):
         obj = os.path.join(obj_dir, os.path.basename(src) + ".o")
@@ -205,6 +209,8 @@ def _build(asan: bool, verbose: bool) -> str:
     link = [CXX, "-shared", "-fPIC", "-o", lib + ".tmp", *[o for o, _, _ in results]]
     if asan:
         link += ["-fsanitize=address", "-shared-libasan"]
+    if cov:
+        link += ["--coverage"]
     r = subprocess.run(link, capture_output=True, text=True)
     if r.returncode:
         raise RuntimeError(f"host link failed:\n{r.stderr}")
@@ -217,4 +223,4 @@ def _build(asan: bool, verbose: bool) -> str:
 
 
 if __name__ == "__main__":
-    build(asan="--asan" in sys.argv)
+    build(asan="--asan" in sys.argv, cov="--cov" in sys.argv)
