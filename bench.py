@@ -160,6 +160,88 @@ def traffic_summarize(d):
         "per_batch": per, "traffic_bytes_per_launch": round(mean)}, indent=1))
 
 
+# instruction-mix counters (two passes of at most eight SQ counters) and the kernels they are read for
+COUNTER_PASSES = {  # six a pass: derived counters can take more than one of the block's eight
+    "insts": ["SQ_INSTS_VALU", "SQ_INSTS_MFMA", "SQ_INSTS_LDS", "SQ_INSTS_SALU", "SQ_WAVES", "SQ_BUSY_CYCLES"],
+    "lds": ["SQ_LDS_BANK_CONFLICT", "SQ_LDS_IDX_ACTIVE", "SQ_VALU_MFMA_BUSY_CYCLES", "SQ_WAIT_ANY",
+            "SQ_ACTIVE_INST_LDS", "SQ_CYCLES"],
+}
+COUNTER_KERNELS = {"prefill": "k_tile_stream", "stack_iq3s": "k_stack_mv"}
+
+
+def counters_run(workload):
+    """The workload an instruction-mix counter run reads: the C5 prefill layer's two stream passes (prefill) or
+    the C2 IQ3_S stream at one token (stack_iq3s), a few launches each."""
+    import numpy as np
+    import torch
+
+    import strata_hip
+    from strata_hip import blocks as SB
+    from strata_hip import fused as SF
+    from strata_hip import synth
+    from strata_hip import tables as T
+
+    strata_hip.load()
+    T.use(T.synthetic(0))
+    dev = torch.device("cuda:0")
+    if workload == "prefill":
+        rng = np.random.default_rng(5)
+        logits = synth.zipf_logits(rng, 2048, E).to(dev)
+        x = torch.from_numpy(rng.standard_normal((2048, D)).astype(np.float32)).to(torch.bfloat16).to(dev)
+        gate = SB.BlockSwitchLinear(synth.random_blocks_gpu("IQ3_S", E * F, D, 11, dev), "IQ3_S", (E, F, D))
+        up = SB.BlockSwitchLinear(synth.random_blocks_gpu("IQ3_S", E * F, D, 12, dev), "IQ3_S", (E, F, D))
+        down = SB.BlockSwitchLinear(synth.random_blocks_gpu("IQ3_S", E * D, F, 13, dev), "IQ3_S", (E, D, F))
+        idx = SF.top_k(logits, K)
+        for _ in range(3):
+            SB._tiled_glu(x[None], idx[None], up, gate, down)
+    elif workload == "stack_iq3s":
+        R, C = 3072, 2048
+        n = -(-600_000_000 // (R * SB.row_bytes("IQ3_S", C)))
+        blocks = synth.random_blocks_gpu("IQ3_S", n * R, C, 7, dev)
+        x = torch.randn(n, 1, C, device=dev).to(torch.bfloat16)
+        for _ in range(3):
+            SB.stack_matvec(blocks, "IQ3_S", (n, R, C), x)
+    else:
+        raise SystemExit(f"--counters-run: {workload} (one of {sorted(COUNTER_KERNELS)})")
+    torch.cuda.synchronize()
+    print(f"{workload}: done", flush=True)
+
+
+def counters_summarize(d, workload):
+    """Markdown: each counter's mean a dispatch of the workload's kernel over the passes' directories under d
+    (d/insts, d/lds), and the ratios read from them."""
+    kernel = COUNTER_KERNELS[workload]
+    mean = {}
+    for pas, names in COUNTER_PASSES.items():
+        for name in names:
+            vals = [v for _, k, v in _counters(os.path.join(d, pas), name) if kernel in k]
+            if vals:
+                mean[name] = sum(vals) / len(vals)
+    if not mean:
+        raise SystemExit(f"no {kernel} dispatches under {d}")
+    lines = [f"# {kernel}: instruction mix ({workload})", "",
+             "Counters a dispatch (rocprofv3 --pmc, two passes; mean over the workload's dispatches):", "",
+             "| counter | a dispatch |", "| :--- | ---: |"]
+    lines += [f"| {k} | {v:,.0f} |" for k, v in mean.items()]
+    mfma = mean.get("SQ_INSTS_MFMA") or 0
+    ratios = []
+    if mfma:
+        for k in ("SQ_INSTS_VALU", "SQ_INSTS_LDS", "SQ_INSTS_SALU"):
+            if k in mean:
+                ratios.append(f"{k} per MFMA: {mean[k] / mfma:.2f}")
+    if mean.get("SQ_INSTS_LDS") and "SQ_LDS_BANK_CONFLICT" in mean:
+        ratios.append(f"LDS bank-conflict cycles per LDS instruction: "
+                      f"{mean['SQ_LDS_BANK_CONFLICT'] / mean['SQ_INSTS_LDS']:.3f}")
+    if mean.get("SQ_BUSY_CYCLES") and "SQ_VALU_MFMA_BUSY_CYCLES" in mean:
+        ratios.append(f"MFMA busy / SQ busy cycles: {mean['SQ_VALU_MFMA_BUSY_CYCLES'] / mean['SQ_BUSY_CYCLES']:.3f}")
+    lines += ["", *[f"- {r}" for r in ratios], "", "Commands (cd /tmp, TMPDIR=/tmp; R the repository root):", ""]
+    for pas, names in COUNTER_PASSES.items():
+        lines.append(f"    timeout -s KILL 120 rocprofv3 --pmc {' '.join(names)} --output-format csv -d $OUT/{pas} "
+                     f"-o {pas} -- python3 $R/bench.py --counters-run {workload}")
+    lines.append(f"    python3 $R/bench.py --counters-summarize $OUT {workload}")
+    print("\n".join(lines))
+
+
 def build_layers(n_layers, dev, kind):
     import torch
 
@@ -611,11 +693,19 @@ def main():
     ap.add_argument("--no-iq3s", action="store_true")
     ap.add_argument("--traffic-run", action="store_true", help="the counter runs' workload (under rocprofv3)")
     ap.add_argument("--traffic-summarize", metavar="DIR", help="the counter summary of two runs' output directory")
+    ap.add_argument("--counters-run", metavar="WORKLOAD", help="an instruction-mix counter run's workload "
+                    "(prefill, stack_iq3s; under rocprofv3)")
+    ap.add_argument("--counters-summarize", nargs=2, metavar=("DIR", "WORKLOAD"),
+                    help="the instruction-mix summary of the two passes' output directory")
     args = ap.parse_args()
     if args.traffic_run:
         return traffic_run()
     if args.traffic_summarize:
         return traffic_summarize(args.traffic_summarize)
+    if args.counters_run:
+        return counters_run(args.counters_run)
+    if args.counters_summarize:
+        return counters_summarize(*args.counters_summarize)
     if args.gpus != 1:
         print(f"bench.py: --gpus {args.gpus}: this path runs and is measured on one GPU (expert parallelism across "
               f"GPUs is not implemented); run with --gpus 1", file=sys.stderr)
