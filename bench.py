@@ -655,6 +655,32 @@ def moe_pass(layers, batches, args, dev, iq3s=False):
                 gu_graph.replay()
             ev[3].record(stream)
             torch.cuda.synchronize()
+            # the windows the down kernel combines itself (2-4 tokens, after a release / acquire hand-off between
+            # its blocks) also timed with the combine as a kernel of its own after the tail: the two forms' costs
+            sep_ms = None
+            if 2 <= b <= 4:
+                from strata_hip import _lib
+
+                lib = _lib.load()
+                before = lib.sh_moe_set_tail_combine(0)
+                try:
+                    sep_graph = torch.cuda.CUDAGraph()
+                    with torch.cuda.graph(sep_graph, stream=stream):
+                        for m, lg, x, o in zip(layers, logits, xs, outs):
+                            m(lg, x, out=o)
+                finally:
+                    lib.sh_moe_set_tail_combine(before)
+                for _ in range(args.warmup):
+                    sep_graph.replay()
+                torch.cuda.synchronize()
+                es = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
+                es[0].record(stream)
+                for _ in range(args.steps):
+                    sep_graph.replay()
+                es[1].record(stream)
+                torch.cuda.synchronize()
+                sep_ms = es[0].elapsed_time(es[1])
+                del sep_graph
             # leave the outputs of a full pass behind (the front's graph rewrote h, not the outputs)
             graph.replay()
             torch.cuda.synchronize()
@@ -666,6 +692,8 @@ def moe_pass(layers, batches, args, dev, iq3s=False):
                         "unique_experts_mean": round(float(np.mean(uniq)), 2),
                         "tok_per_s": round(b * args.steps / (ms * 1e-3), 1),
                         "front_us": round(gu_ms * 1e3 / n_layers, 3)}
+        if sep_ms is not None:
+            per_batch[b]["us_per_layer_combine_kernel"] = round(sep_ms * 1e3 / n_layers, 3)
         all_bytes += bytes_pass * args.steps
         all_time += ms * 1e-3
         gu_bytes += sum(front_bytes(u, b, kind_bytes) for u in uniq) * args.steps
