@@ -264,3 +264,34 @@ def test_window_matvec_bits_do_not_depend_on_the_window(kind, tables, dev):
     alone = torch.cat([SB.window_matvec(b, kind, 96, 2048, x[t:t + 1].to(dev)).cpu() for t in range(8)])
     assert torch.equal(alone, got)
     assert rel_err(got.float(), x.float().numpy().astype(np.float64) @ w[0].T.astype(np.float64)) <= 1e-2
+
+
+@pytest.mark.parametrize("kind, dtype", [("Q2_0", "bfloat16"), ("IQ3_S", "float16"), ("IQ4_NL", "bfloat16"),
+                                         ("Q2_0", "float32"), ("Q3_K", "float16")])
+def test_pairs_naming_no_expert_get_zeros(kind, dtype, tables, dev):
+    """A pair whose index is outside 0..experts-1 reads no weights and gets a zero row (every product kernel: the
+    MFMA and generic matvecs, the GLU matvec, the table-of-sums products); the other pairs are the oracle's."""
+    E, R, C = 4, 48, 512
+    raw, w = stack(kind, E, R, C, 31, tables)
+    rng = np.random.default_rng(32)
+    idx = np.array([2, -1, 0, E, 3, 1 << 20, 1])
+    x, xv = act(rng, (len(idx), C), dtype)
+    lin = SB.BlockSwitchLinear(torch.from_numpy(raw).to(dev), kind, (E, R, C))
+    ti = torch.from_numpy(idx).to(dev)
+    real = (idx >= 0) & (idx < E)
+    got = SB.switch_matvec(lin.blocks, kind, (E, R, C), ti, x.to(dev), 1).float().cpu().numpy()
+    assert (got[~real] == 0).all()
+    assert rel_err(got[real], OB.matvec(w, idx[real], xv[real], 1)) <= TOL[dtype]
+    if dtype == "float32":
+        return
+    u, uv = act(rng, (len(idx), C), dtype)
+    glu = SB.matvec_glu(lin, ti, x.to(dev), u.to(dev)).float().cpu().numpy()
+    assert (glu[~real] == 0).all()
+    assert rel_err(glu[real], OB.matvec(w, idx[real], OR.swiglu(xv, uv, dtype)[real], 1)) <= TOL[dtype]
+    if kind == "Q2_0" and dtype == "bfloat16":
+        xh = x.to(torch.float16)
+        look = SB.lookup_matvec(lin, ti, SB.lookup_table(xh.to(dev)), 1).float().cpu().numpy()
+        assert (look[~real] == 0).all()
+        assert rel_err(look[real], OB.matvec(w, idx[real], xh.float().numpy()[real], 1)) <= 1e-2
+        down = SB.lookup_down_glu(lin, ti, xh.to(dev), u.to(torch.float16).to(dev)).float().cpu().numpy()
+        assert (down[~real] == 0).all()
