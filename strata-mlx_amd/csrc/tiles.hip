@@ -213,7 +213,9 @@ static int launch_tiles(const uint8_t* blocks, const uint8_t* tables, int64_t ex
 // Modes: TS_PLAIN is tile_matmul (a in slot order, float32 rows of the slots out); TS_GLU takes a token's row of
 // x for each slot, runs gate and up (32 rows of each an item) and writes silu(g) * u rounded to x's type in slot
 // order; TS_DOWN takes those rows and writes each pair's row, rounded to x's type, where the slot's pair is.
-enum { TS_PLAIN = 0, TS_GLU = 1, TS_DOWN = 2 };
+// TS_DOWN_S is TS_DOWN with a short unit's tiles shared among consumers, its activation fragments loaded one step
+// ahead into one register buffer instead of two steps ahead into two (the registers the sharing needs).
+enum { TS_PLAIN = 0, TS_GLU = 1, TS_DOWN = 2, TS_DOWN_S = 3 };
 constexpr int TS_KCH = 256, TS_RBV = 64, TS_TGU = 8, TS_NR = 6, TS_LEAD = 5, TS_NT = 1024;
 constexpr int TS_WT = 3 * TS_NT;                      // tiles of a window: three a thread in the layout
 constexpr int TS_PPR = 8;                             // 16-byte pieces a row's chunk may cover
@@ -286,6 +288,8 @@ template <int KIND, typename XT, int MODE>
 __global__ __launch_bounds__(TS_NT) void k_tile_stream(TileStreamArgs g) {
   constexpr int CB = ts_chunk_bytes<KIND>(), TAB = ts_tab_bytes<KIND>(), TPT = TS_WT / TS_NT;
   constexpr int VR = MODE == TS_GLU ? TS_RBV / 2 : TS_RBV;  // rows of one stack an item
+  constexpr bool DOWN = MODE == TS_DOWN || MODE == TS_DOWN_S;
+  constexpr int ABUF = MODE == TS_DOWN_S ? 1 : 2;  // activation fragment buffers: steps loaded ahead
   static_assert(CB + 15 <= TS_PPR * 16, "a row's chunk fits its ring row");
   extern __shared__ u32x4 dyn[];
   uint8_t* lds = (uint8_t*)dyn;
@@ -458,14 +462,14 @@ __global__ __launch_bounds__(TS_NT) void k_tile_stream(TileStreamArgs g) {
       // chunk q are in af[q & 1], loaded two steps ahead (the loop is unrolled by two: the buffers stay registers)
       const int cw = wave - 8;
       auto wpt_of = [&](int len) {  // (TS_DOWN: one wave a tile; its registers are at the limit already)
-        constexpr int MAXW = MODE == TS_PLAIN ? 4 : MODE == TS_GLU ? 2 : 1;
+        constexpr int MAXW = MODE == TS_PLAIN || MODE == TS_DOWN_S ? 4 : MODE == TS_GLU ? 2 : 1;
         return !g.share ? 1 : len <= 2 ? MAXW : len <= 4 ? min(2, MAXW) : 1;
       };
       auto tile_of = [&](int len) { return cw / wpt_of(len); };
       const XT* a = (const XT*)g.a;
       f32x4 acc[4];
       int pr[4] = {0, 0, 0, 0};  // TS_DOWN: the output rows of the lane's four slots in the current item
-      u32x4 af[2][TS_KCH / 32];
+      u32x4 af[ABUF][TS_KCH / 32];
       const XT* arow = a;
 #pragma unroll
       for (int f = 0; f < 4; ++f) acc[f] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
@@ -540,7 +544,7 @@ __global__ __launch_bounds__(TS_NT) void k_tile_stream(TileStreamArgs g) {
             for (int j = 0; j < NF; ++j) acc[j] = mfma<XT>(af[BUF][ks], b[ks & 1][j], acc[j]);
           }
           const int64_t slot0 = (int64_t)(s.start + tl) * TILE_TOKENS + 4 * gq;
-          if constexpr (MODE == TS_DOWN) {  // the slots' output rows, at the item's first chunk
+          if constexpr (DOWN) {  // the slots' output rows, at the item's first chunk
             if (s.c == 0) {
 #pragma unroll
               for (int i = 0; i < 4; ++i) pr[i] = g.pair[slot0 + i];
@@ -573,7 +577,7 @@ __global__ __launch_bounds__(TS_NT) void k_tile_stream(TileStreamArgs g) {
             for (int f = 0; f < 4; ++f) acc[f] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
           }
         };
-        if constexpr (MODE == TS_DOWN) {
+        if constexpr (MODE == TS_DOWN) {  // (TS_DOWN_S takes the shared forms below)
           multiply(std::integral_constant<int, 1>{});
         } else {
           const int wpt = wpt_of(s.len);
@@ -586,7 +590,7 @@ __global__ __launch_bounds__(TS_NT) void k_tile_stream(TileStreamArgs g) {
         }
         __builtin_amdgcn_sched_barrier(0);  // chunk q + 2's fragments load after chunk q's are consumed
         cur_next(cs);
-        if (cl.q < Q) {  // cl.q == q + 2
+        if (cl.q < Q) {  // cl.q == q + ABUF
           load_a(cl, bc);
           cur_next(cl);
         }
@@ -595,18 +599,24 @@ __global__ __launch_bounds__(TS_NT) void k_tile_stream(TileStreamArgs g) {
       using B1 = std::integral_constant<int, 1>;
       load_a(cl, B0{});
       cur_next(cl);
-      if (Q > 1) {
-        load_a(cl, B1{});
-        cur_next(cl);
+      if constexpr (ABUF == 2) {
+        if (Q > 1) {
+          load_a(cl, B1{});
+          cur_next(cl);
+        }
       }
       if constexpr (KIND == IQ3_S) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // (the table)
       lds_sync();
       int q = 0;
-      for (; q + 1 < Q; q += 2) {
-        step(B0{});
-        step(B1{});
+      if constexpr (ABUF == 2) {
+        for (; q + 1 < Q; q += 2) {
+          step(B0{});
+          step(B1{});
+        }
+        if (q < Q) step(B0{});
+      } else {
+        for (; q < Q; ++q) step(B0{});
       }
-      if (q < Q) step(B0{});
       // nothing of the consumers' left in flight where the compiler joins the roles' paths: its waits in the
       // producers' code would count against their ring loads
       __builtin_amdgcn_s_waitcnt(0);
@@ -741,6 +751,9 @@ int sh_tile_down(int kind, const void* down, const void* tables, int64_t experts
   g.n_tiles = (int)(slots / TILE_TOKENS), g.n_src = pairs;
   return with_half_dtype(h_dtype, [&](auto* tp) {
     using XT = std::remove_pointer_t<decltype(tp)>;
+    if (g_share.load(std::memory_order_relaxed))
+      return kind == IQ3_S ? launch_stream<IQ3_S, XT, TS_DOWN_S>(g, (hipStream_t)stream, "tile_down")
+                           : launch_stream<Q2_0, XT, TS_DOWN_S>(g, (hipStream_t)stream, "tile_down");
     return kind == IQ3_S ? launch_stream<IQ3_S, XT, TS_DOWN>(g, (hipStream_t)stream, "tile_down")
                          : launch_stream<Q2_0, XT, TS_DOWN>(g, (hipStream_t)stream, "tile_down");
   });

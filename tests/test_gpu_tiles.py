@@ -186,8 +186,8 @@ def test_a_float32_prompt_through_the_tiles(tables, dev):
 @pytest.mark.parametrize("kind, dtype", [("IQ3_S", torch.bfloat16), ("Q2_0", torch.float16)])
 def test_shared_tiles_give_one_wave_a_tiles_bits(kind, dtype, tables, dev):
     """Experts' runs of 1-8 tiles (Zipf routing over few experts): the streamed products with a short run's tiles
-    shared among waves (each wave some of the 64 rows) give the bits of one wave a tile, for tile_matmul and for
-    the fused gate / up + SwiGLU, call after call."""
+    shared among waves (each wave some of the 64 rows) give the bits of one wave a tile, for tile_matmul, the fused
+    gate / up + SwiGLU and the down pass, call after call."""
     from strata_hip import _lib
 
     E, F, D, T, K = 24, 256, 512, 96, 6
@@ -205,12 +205,13 @@ def test_shared_tiles_give_one_wave_a_tiles_bits(kind, dtype, tables, dev):
     lib = _lib.load()
     before = lib.sh_tiles_set_share(1)
     try:
-        shared = (SB.tile_matmul(raws["g"], kind, (E, F, D), a, te)[valid],
-                  SB.tile_glu(lin["g"], lin["u"], x, token, te)[valid])
+        h = SB.tile_glu(lin["g"], lin["u"], x, token, te)
+        shared = (SB.tile_matmul(raws["g"], kind, (E, F, D), a, te)[valid], h[valid],
+                  SB.tile_down(lin["d"], h, te, where))
         torch.cuda.synchronize()
         lib.sh_tiles_set_share(0)
         alone = (SB.tile_matmul(raws["g"], kind, (E, F, D), a, te)[valid],
-                 SB.tile_glu(lin["g"], lin["u"], x, token, te)[valid])
+                 SB.tile_glu(lin["g"], lin["u"], x, token, te)[valid], SB.tile_down(lin["d"], h, te, where))
         torch.cuda.synchronize()
         lib.sh_tiles_set_share(1)
         again = SB.tile_glu(lin["g"], lin["u"], x, token, te)[valid]
@@ -218,4 +219,5 @@ def test_shared_tiles_give_one_wave_a_tiles_bits(kind, dtype, tables, dev):
         lib.sh_tiles_set_share(before)
     assert torch.equal(shared[0], alone[0])
     assert torch.equal(shared[1].view(torch.int16), alone[1].view(torch.int16))
+    assert torch.equal(shared[2].view(torch.int16), alone[2].view(torch.int16))
     assert torch.equal(again.view(torch.int16), shared[1].view(torch.int16))
