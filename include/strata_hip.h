@@ -214,9 +214,10 @@ int sh_tile_down(int kind, const void* down, const void* tables, int64_t experts
                  const void* h, int h_dtype, int64_t slots, const int32_t* tile_expert, const int32_t* pair,
                  int64_t pairs, void* out, void* stream);
 /* No counterpart in the reference (a tuning knob for callers and tests): whether the streamed tile products
- * (sh_tile_matmul, sh_tile_glu of Q2_0 / IQ3_S) share the tiles of an expert's run of at most four tiles among
- * several multiplying waves (on by default) or give each tile one wave. Both give the same bits. Returns the
- * previous setting. Process-wide; not for use while another thread launches them. */
+ * (sh_tile_matmul, sh_tile_glu, sh_tile_down of Q2_0 / IQ3_S) share the tiles of an expert's run of at most four
+ * tiles among several multiplying waves (on by default) or give each tile one wave. Both give the same bits. Read
+ * at launch (a captured graph keeps the form it was captured with). Returns the previous setting. Process-wide;
+ * not for use while another thread launches them. */
 int sh_tiles_set_share(int on);
 
 /* ---- dense layers: Q6_K held as three parts (strata_mlx/dense.py:109-167, ScaledLinear), w[r][c] = code[r][c] *
