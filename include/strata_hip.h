@@ -149,7 +149,8 @@ int sh_tiles_of(const int32_t* idx, int64_t pairs, int64_t k, int64_t experts, i
  * combine (fused.py:448-481). No host synchronisation: for 512 experts, d_model 2048, d_ff 512 (16-byte aligned
  * operands) two kernels (route + gate/up + SwiGLU, then down + combine), otherwise three (route; gate/up; down +
  * combine). kind / kind_down: Q2_0 or IQ3_S; dtype: F16 or BF16;
- * d_model, d_ff multiples of 256; experts a multiple of 64 up to 2048. idx_out (tokens x k int32) and w_out
+ * d_model and d_ff whole blocks of the kinds that read them (64 weights a Q2_0 block, 256 an IQ3_S one: the reference
+ * model's 2560 / 640 with Q2_0 down); experts a multiple of 64 up to 2048. idx_out (tokens x k int32) and w_out
  * (tokens x k float32) are optional copies of the choice. workspace: sh_moe_workspace() bytes, zeroed once before
  * its first call (the launch's counters, at its head whatever the shape, must start at zero; every call leaves them
  * at zero, so one workspace serves calls of any shape in turn); calls sharing a workspace must not overlap. */

@@ -1598,9 +1598,12 @@ int moe_decode(int phases, int kind, int kind_down, const void* gate, const void
                 (long long)k, MOE_MAX_TOKENS, MOE_MAX_PAIRS);
   if (experts <= 0 || vpl_bad(experts) || k > experts)
     return fail(E_SHAPE, "moe_decode: %lld experts (64 times a power of two, at most 2048)", (long long)experts);
-  if (d_model % 256 || d_ff % 256 || d_model <= 0 || d_ff <= 0 || d_model > MOE_MAX_D)
-    return fail(E_SHAPE, "moe_decode: widths %lld / %lld (multiples of 256, d_model at most %d)", (long long)d_model,
-                (long long)d_ff, MOE_MAX_D);
+  // widths: whole blocks of the kinds that read them (gate / up rows of d_model, down rows of d_ff: 64 weights a
+  // Q2_0 block, 256 an IQ3_S one), d_ff in 16-row tiles of gate / up (the reference model's 2560 / 640 with Q2_0 down)
+  if (d_model <= 0 || d_ff <= 0 || d_model > MOE_MAX_D || d_model % (kind == IQ3_S ? 256 : 64) ||
+      d_ff % (kind_down == IQ3_S ? 256 : 64))
+    return fail(E_SHAPE, "moe_decode: widths %lld / %lld (whole blocks of their kinds, d_model at most %d)",
+                (long long)d_model, (long long)d_ff, MOE_MAX_D);
   if (!mfma_kind_host(kind) || !mfma_kind_host(kind_down))
     return fail(E_UNSUPPORTED, "moe_decode: kinds %d / %d (the fused step takes Q2_0 and IQ3_S)", kind, kind_down);
   if (!gate || !up || !down || !shared_gate || !shared_up || !shared_down || !shared_gate_w || !logits || !x || !out)

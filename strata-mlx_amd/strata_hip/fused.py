@@ -202,8 +202,9 @@ class MoEDecode:
         v = self.experts // 64
         return (0 < tokens <= self.MAX_TOKENS and tokens * self.k <= 160 and x.dtype in (torch.float16, torch.bfloat16)
                 and self.gate.kind in ("Q2_0", "IQ3_S") and self.down.kind in ("Q2_0", "IQ3_S")
-                and self.experts % 64 == 0 and 1 <= v <= 32 and v & (v - 1) == 0 and self.d_model % 256 == 0
-                and self.d_model <= 8192 and self.d_ff % 256 == 0)
+                and self.experts % 64 == 0 and 1 <= v <= 32 and v & (v - 1) == 0
+                and self.d_model % (256 if self.gate.kind == "IQ3_S" else 64) == 0 and self.d_model <= 8192
+                and self.d_ff % (256 if self.down.kind == "IQ3_S" else 64) == 0)
 
     def workspace(self, tokens: int, dtype: torch.dtype, device) -> torch.Tensor:
         key = (tokens, dtype, str(device))
