@@ -203,22 +203,40 @@ __device__ __forceinline__ void item_mac(const uint8_t* wrow0, int rstride, cons
       dh[j] = *(const uint16_t*)b;
     }
   } else {
-    uint32_t q2[GPER], qh[GPER], sg[GPER];
+    static_assert(KIND != IQ3_S || GPER % 8 == 0, "IQ3_S: whole superblocks a wave");
+    // a superblock's header once: its eight high-bit bytes as two words, its four scale bytes as one
+    uint32_t q2[GPER], sg[GPER], qd[GPER / 4];
 #pragma unroll
     for (int j = 0; j < GPER; ++j) {
       const uint8_t* b = wrow + (j >> 3) * 110;
       const int ib = j & 7;
       q2[j] = *(const uint16_t*)(b + 2 + 8 * ib + 2 * g);
-      qh[j] = b[66 + ib];
       sg[j] = b[74 + 4 * ib + g];
-      if (ib % 2 == 0) sc[j] = b[106 + ib / 2];
-      if (ib == 0) dh[j] = *(const uint16_t*)b;
+      if (ib % 4 == 0)
+        qd[j / 4] = (uint32_t)b[66 + ib] | ((uint32_t)b[67 + ib] << 8) | ((uint32_t)b[68 + ib] << 16) |
+                    ((uint32_t)b[69 + ib] << 24);
+      if (ib == 0) {
+        dh[j] = *(const uint16_t*)b;
+        sc[j] = (uint32_t)b[106] | ((uint32_t)b[107] << 8) | ((uint32_t)b[108] << 16) | ((uint32_t)b[109] << 24);
+      }
     }
+    // The two grid indices of run j, (low byte | high bit << 8 | sign nibble << 9), built side by side as the two
+    // halves of one word: the high bits of four runs spread to bit 0 of a byte each (E: the first index's, O: the
+    // second's), a byte permute picks run j's pair, the sign nibbles go to bits 1-4 of their bytes, and a second
+    // permute interleaves those bytes with the low bytes.
 #pragma unroll
-    for (int j = 0; j < GPER; ++j) {
-      const uint32_t h = qh[j] >> (2 * g);
-      w0[j] = stab[(q2[j] & 0xffu) | ((h & 1u) << 8) | ((sg[j] & 15u) << 9)];
-      w1[j] = stab[(q2[j] >> 8) | ((h & 2u) << 7) | ((sg[j] >> 4) << 9)];
+    for (int j4 = 0; j4 < GPER / 4; ++j4) {
+      const uint32_t qs = qd[j4] >> (2 * g);
+      const uint32_t E = qs & 0x01010101u, O = (qs >> 1) & 0x01010101u;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int j = 4 * j4 + r;
+        const uint32_t hr = __builtin_amdgcn_perm(O, E, 0x0c0c0000u | ((uint32_t)(4 + r) << 8) | (uint32_t)r);
+        const uint32_t t = (((sg[j] << 1) | (sg[j] << 5)) & 0x1e1eu) | hr;
+        const uint32_t w = __builtin_amdgcn_perm(t, q2[j], 0x05010400u);
+        w0[j] = stab[w & 0xffffu];
+        w1[j] = stab[w >> 16];
+      }
     }
   }
   f32x4 D[2] = {{0.0f, 0.0f, 0.0f, 0.0f}, {0.0f, 0.0f, 0.0f, 0.0f}};
@@ -274,8 +292,12 @@ __device__ __forceinline__ void item_mac(const uint8_t* wrow0, int rstride, cons
     if constexpr (KIND == Q2_0) {
       dprev = half_bits(dh[j]);
     } else {
+      // 1 + 2 x the run's scale nibble: the superblock's four scale bytes turned into those values for the even
+      // runs (low nibbles) and the odd runs (high nibbles), a byte each
       const int ib = j & 7;
-      dprev = half_bits(dh[j & ~7]) * (float)(1 + 2 * ((sc[j & ~1] >> (4 * (ib & 1))) & 15u));
+      const uint32_t s4 = sc[j & ~7];
+      const uint32_t odd = ib & 1 ? (s4 >> 3) & 0x1e1e1e1eu : (s4 << 1) & 0x1e1e1e1eu;
+      dprev = half_bits(dh[j & ~7]) * (float)(((odd | 0x01010101u) >> (8 * (ib >> 1))) & 0xffu);
     }
   }
 #pragma unroll
