@@ -76,12 +76,18 @@ int sh_switch_matvec_generic(int kind, const void* blocks, const void* const* ex
                              const void* x, int x_dtype, int64_t share, void* out, void* stream);
 
 /* strata_mlx/blocks.py:351-394 (window_matvec) over a stack: out[m][t] = W_m . x[m][t], x (n_mats, tokens <= 16,
- * cols) bf16 / fp16, out (n_mats, tokens, rows); Q2_0 or IQ3_S, cols a multiple of 256. One streaming launch over
- * all matrices (and a staging launch for x). workspace: sh_stack_workspace() bytes. */
+ * cols) bf16 / fp16, out (n_mats, tokens, rows); Q2_0 or IQ3_S, cols a multiple of 256 up to 4096 (wider rows where
+ * the waves' column splits and the LDS ring allow: sh_stack_takes says). One streaming launch over all matrices
+ * (one per window of row tiles for the longest Q2_0 stacks). workspace: sh_stack_workspace() bytes (none). */
 size_t sh_stack_workspace(int kind, int64_t n_mats, int64_t rows, int64_t cols, int64_t tokens, int x_dtype);
 int sh_stack_matvec(int kind, const void* blocks, const void* tables, int64_t n_mats, int64_t rows, int64_t cols,
                     const void* x, int x_dtype, int64_t tokens, void* out, void* workspace, size_t workspace_bytes,
                     void* stream);
+/* No counterpart in the reference, whose window matvec (strata_mlx/blocks.py:351-394) takes rows of every width:
+ * 1 if sh_stack_matvec takes these arguments, 0 if it refuses them (its checks and launch plan, nothing launched),
+ * for a caller choosing between it and sh_window_matvec. */
+int sh_stack_takes(int kind, const void* blocks, const void* tables, int64_t n_mats, int64_t rows, int64_t cols,
+                   const void* x, int x_dtype, int64_t tokens);
 
 /* strata_mlx/blocks.py:331-346 (matvec_separate): one expert buffer per pair, `expert_ptrs` a device array of
  * `pairs` pointers. */

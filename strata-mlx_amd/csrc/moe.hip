@@ -388,8 +388,10 @@ __global__ __launch_bounds__(256) void k_moe_gate_up(const uint8_t* __restrict__
 #pragma unroll
   for (int i = 0; i < TPG; ++i) acc[0][i] = acc[1][i] = 0.0f;
   const uint8_t* tiles[2] = {wg + lead_of(g_src), wu + lead_of(u_src)};
-  const int per = D / scale_group<KIND>() / 4;
-  tile_mac_global<KIND, MT, TPG, frag_chunk<KIND>(), 2>(tiles, (int)rb, xg, real, wave * per, (wave + 1) * per,
+  // the row's scale groups split four ways, the parts differing by at most one group (a row of fewer than four
+  // groups leaves some waves none)
+  const int ng = D / scale_group<KIND>();
+  tile_mac_global<KIND, MT, TPG, frag_chunk<KIND>(), 2>(tiles, (int)rb, xg, real, wave * ng / 4, (wave + 1) * ng / 4,
                                                          (const uint32_t*)tab, acc);
 #pragma unroll
   for (int i = 0; i < TPG; ++i) {

@@ -397,7 +397,7 @@ __global__ __launch_bounds__(SQ_WAVES * 64) void k_stack_q2(const uint8_t* __res
 
 template <typename XT, int RT>
 static int launch_stack_q2(const uint8_t* blocks, int64_t n_mats, int64_t rows, int64_t cols, const XT* x,
-                           int64_t tokens, XT* out, hipStream_t stream) {
+                           int64_t tokens, XT* out, hipStream_t stream, bool dry) {
   constexpr int TR = 16 * RT;
   constexpr size_t ring = (size_t)SQ_WAVES * sq_ns<RT>() * sq_slot<RT>();
   SqPlan P{};
@@ -433,6 +433,7 @@ static int launch_stack_q2(const uint8_t* blocks, int64_t n_mats, int64_t rows, 
   P.ring_off = (int)(lds - ring);
   if (lds > 128 * 1024)
     return fail(E_UNSUPPORTED, "stack_matvec: ring past the direct-load range");
+  if (dry) return OK;
   const int64_t grid = (int64_t)cus * per_cu, window = grid * per;
   for (int64_t r = 0; r < P.total; r += window) {
     P.rg0 = (int)r;
@@ -446,7 +447,7 @@ static int launch_stack_q2(const uint8_t* blocks, int64_t n_mats, int64_t rows, 
 
 template <int KIND, typename XT, int TPG, int GPER, int RW>
 static int launch_stack(const uint8_t* blocks, const uint8_t* tables, int64_t n_mats, int64_t rows, int64_t cols,
-                        const XT* x, int64_t tokens, XT* out, bool few, hipStream_t stream) {
+                        const XT* x, int64_t tokens, XT* out, bool few, hipStream_t stream, bool dry) {
   StackPlan P;
   P.rows = (int)rows;
   P.cols = (int)cols;
@@ -487,6 +488,7 @@ static int launch_stack(const uint8_t* blocks, const uint8_t* tables, int64_t n_
   P.red_off = P.ring_off + P.nbuf * P.buf_bytes;
   const size_t lds = (size_t)P.red_off + red + tail;
   if (lds > cap) return fail(E_UNSUPPORTED, "stack_matvec: %zu bytes of LDS", lds);
+  if (dry) return OK;
   auto run = [&](auto kern) {
     int per_cu = 0;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, nt, lds) != hipSuccess || per_cu < 1) per_cu = 1;
@@ -508,9 +510,11 @@ size_t sh_stack_workspace(int kind, int64_t n_mats, int64_t rows, int64_t cols, 
   return 0;
 }
 
-int sh_stack_matvec(int kind, const void* blocks, const void* tables, int64_t n_mats, int64_t rows, int64_t cols,
-                    const void* x, int x_dtype, int64_t tokens, void* out, void* workspace, size_t workspace_bytes,
-                    void* stream) {
+}  // extern "C"
+
+// The stack matvec's checks and plan, then its launches (dry: the checks and the plan only, nothing launched).
+static int stack_matvec(bool dry, int kind, const void* blocks, const void* tables, int64_t n_mats, int64_t rows,
+                        int64_t cols, const void* x, int x_dtype, int64_t tokens, void* out, void* stream) {
   int st = check_rows(kind, rows, cols, "stack_matvec");
   if (st) return st;
   if (n_mats <= 0 || tokens <= 0) return OK;
@@ -521,7 +525,7 @@ int sh_stack_matvec(int kind, const void* blocks, const void* tables, int64_t n_
   if (!mfma_kind_host(kind) || (x_dtype != BF16 && x_dtype != F16) || cols % 256)
     return fail(E_UNSUPPORTED, "stack_matvec: kind %d, dtype %d, %lld columns (Q2_0 / IQ3_S, bf16 / fp16, columns a "
                 "multiple of 256)", kind, x_dtype, (long long)cols);
-  if (!blocks || !x || !out || (kind == IQ3_S && !tables)) return fail(E_ARG, "stack_matvec: null pointer");
+  if (!blocks || !x || (!out && !dry) || (kind == IQ3_S && !tables)) return fail(E_ARG, "stack_matvec: null pointer");
   if (((uintptr_t)x & 15) || (tables && ((uintptr_t)tables & 15)))
     return fail(E_ARG, "stack_matvec: activations and tables must be 16-byte aligned");
   // a wave's columns: GPER scale groups (8 or 4 Q2_0 blocks, 16 or 8 IQ3_S runs), at most 16 waves across a row
@@ -533,9 +537,10 @@ int sh_stack_matvec(int kind, const void* blocks, const void* tables, int64_t n_
   const int64_t small = 4;
   const bool rw2_shape = kind == Q2_0 && tokens <= 4 && ngroups % small == 0 && ngroups / small <= 8;
   const int gper1 = kind == Q2_0 ? (ngroups % 8 == 0 ? 8 : 4) : (ngroups % 8 == 0 && ngroups / 8 <= 16 ? 8 : 16);
-  if (ngroups / gper1 > 16)
-    return fail(E_UNSUPPORTED, "stack_matvec: %lld columns (at most %d)", (long long)cols,
-                16 * gper1 * (kind == Q2_0 ? 64 : 32));
+  // the groups split evenly over the waves: IQ3_S rows past 4096 columns (16 runs a wave) in whole 512s
+  if (ngroups / gper1 > 16 || ngroups % gper1)
+    return fail(E_UNSUPPORTED, "stack_matvec: %lld columns (at most %d%s)", (long long)cols,
+                16 * gper1 * (kind == Q2_0 ? 64 : 32), kind == IQ3_S ? ", past 4096 a multiple of 512" : "");
   const int tpg = tokens <= 4 ? 1 : tokens <= 8 ? 2 : 4;
   // few items to go round the CUs: one row group a block, one item a block
   const int64_t kw1 = ngroups / gper1, ir = rw2_shape ? 32 : 16 * std::max<int64_t>(1, (kind == Q2_0 ? 8 : 16) / kw1);
@@ -551,17 +556,17 @@ int sh_stack_matvec(int kind, const void* blocks, const void* tables, int64_t n_
     using XT = std::remove_pointer_t<decltype(tp)>;
     if (q2_stream && rows % 32 == 0)
       return launch_stack_q2<XT, 2>((const uint8_t*)blocks, n_mats, rows, cols, (const XT*)x, tokens, (XT*)out,
-                                    (hipStream_t)stream);
+                                    (hipStream_t)stream, dry);
     if (q2_stream)
       return launch_stack_q2<XT, 1>((const uint8_t*)blocks, n_mats, rows, cols, (const XT*)x, tokens, (XT*)out,
-                                    (hipStream_t)stream);
+                                    (hipStream_t)stream, dry);
     auto go = [&](auto kc, auto gc, auto tc) {
       constexpr int K = decltype(kc)::value, G = decltype(gc)::value, T = decltype(tc)::value;
       if (rw2)
         return launch_stack<K, XT, T, G, 2>((const uint8_t*)blocks, (const uint8_t*)tables, n_mats, rows, cols,
-                                            (const XT*)x, tokens, (XT*)out, few, (hipStream_t)stream);
+                                            (const XT*)x, tokens, (XT*)out, few, (hipStream_t)stream, dry);
       return launch_stack<K, XT, T, G, 1>((const uint8_t*)blocks, (const uint8_t*)tables, n_mats, rows, cols,
-                                          (const XT*)x, tokens, (XT*)out, few, (hipStream_t)stream);
+                                          (const XT*)x, tokens, (XT*)out, few, (hipStream_t)stream, dry);
     };
     auto by_t = [&](auto kc, auto gc) {
       return tpg == 1 ? go(kc, gc, kind_c<1>{}) : tpg == 2 ? go(kc, gc, kind_c<2>{}) : go(kc, gc, kind_c<4>{});
@@ -569,6 +574,19 @@ int sh_stack_matvec(int kind, const void* blocks, const void* tables, int64_t n_
     if (kind == Q2_0) return gper == 8 ? by_t(kind_c<Q2_0>{}, kind_c<8>{}) : by_t(kind_c<Q2_0>{}, kind_c<4>{});
     return gper == 16 ? by_t(kind_c<IQ3_S>{}, kind_c<16>{}) : by_t(kind_c<IQ3_S>{}, kind_c<8>{});
   });
+}
+
+extern "C" {
+
+int sh_stack_matvec(int kind, const void* blocks, const void* tables, int64_t n_mats, int64_t rows, int64_t cols,
+                    const void* x, int x_dtype, int64_t tokens, void* out, void* workspace, size_t workspace_bytes,
+                    void* stream) {
+  return stack_matvec(false, kind, blocks, tables, n_mats, rows, cols, x, x_dtype, tokens, out, stream);
+}
+
+int sh_stack_takes(int kind, const void* blocks, const void* tables, int64_t n_mats, int64_t rows, int64_t cols,
+                   const void* x, int x_dtype, int64_t tokens) {
+  return stack_matvec(true, kind, blocks, tables, n_mats, rows, cols, x, x_dtype, tokens, nullptr, nullptr) == OK;
 }
 
 }  // extern "C"

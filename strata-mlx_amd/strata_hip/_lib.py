@@ -46,6 +46,7 @@ PROTOTYPES = {
                       c_i64, c_i64, c_i64, c_i64, c_vp, c_vp, c_vp, c_vp, c_sz, c_vp],
     "sh_stack_workspace": [c_int, c_i64, c_i64, c_i64, c_i64, c_int],
     "sh_stack_matvec": [c_int, c_vp, c_vp, c_i64, c_i64, c_i64, c_vp, c_int, c_i64, c_vp, c_vp, c_sz, c_vp],
+    "sh_stack_takes": [c_int, c_vp, c_vp, c_i64, c_i64, c_i64, c_vp, c_int, c_i64],
     "sh_moe_decode_phase": [c_int, c_int, c_int, c_vp, c_vp, c_vp, c_i64, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_int,
                             c_vp, c_int, c_i64, c_i64, c_i64, c_i64, c_vp, c_vp, c_sz, c_vp],
     "sh_moe_set_tail_combine": [c_int],

@@ -171,6 +171,14 @@ def stack_matvec(blocks: torch.Tensor, kind: str, shape: tuple, x: torch.Tensor)
     return out
 
 
+def _stack_plans(blocks: torch.Tensor, kind: str, rows: int, cols: int, x: torch.Tensor) -> bool:
+    """Whether the streaming stack kernel has a plan for this one layer (its waves' column splits and LDS ring hold
+    the row); wider rows take the generic window kernel."""
+    _on_gpu(blocks, x)
+    return bool(_lib.load().sh_stack_takes(_kind(kind), _u8(blocks).data_ptr(), _tabs(kind, x.device), 1, rows, cols,
+                                           x.data_ptr(), _lib.dtype_code(x.dtype), x.shape[0]))
+
+
 def window_matvec(blocks: torch.Tensor, kind: str, rows: int, cols: int, x: torch.Tensor,
                   per_row: int | None = None) -> torch.Tensor:
     """out[t] = W . x[t] for one layer `blocks` of (rows, cols) and x (tokens, cols). Returns (tokens, rows)
@@ -180,7 +188,7 @@ def window_matvec(blocks: torch.Tensor, kind: str, rows: int, cols: int, x: torc
     _check_stack(blocks, kind, 1, rows, cols, "window_matvec")
     x = x.reshape(-1, cols).contiguous()
     tokens = x.shape[0]
-    if stack_takes(kind, cols, x.dtype) and 0 < tokens <= 16:
+    if stack_takes(kind, cols, x.dtype) and 0 < tokens <= 16 and _stack_plans(blocks, kind, rows, cols, x):
         return stack_matvec(blocks, kind, (1, rows, cols), x[None])[0]
     _on_gpu(blocks, x)
     out = torch.empty((tokens, rows), dtype=x.dtype, device=x.device)

@@ -19,7 +19,8 @@ NAME = {torch.float16: "float16", torch.bfloat16: "bfloat16"}
 
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
-@pytest.mark.parametrize("D, rot, stride_mul", [(256, 64, 2), (128, 128, 1), (256, 0, 1)])
+@pytest.mark.parametrize("D, rot, stride_mul", [(256, 64, 2), (128, 128, 1), (256, 0, 1), (64, 64, 1), (192, 32, 1),
+                                                (320, 320, 2), (384, 0, 1), (448, 64, 1), (512, 128, 1)])
 def test_qk_rope_is_the_oracles(dtype, D, rot, stride_mul, dev):
     rng = np.random.default_rng(D + rot)
     S, H = 5, 6

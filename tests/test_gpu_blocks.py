@@ -255,6 +255,43 @@ def test_long_stacks_stream_by_waves(kind, shape, tokens, dtype, tables, dev):
         assert rel_err(got[m], want[m]) <= TOL[dtype]
 
 
+@pytest.mark.parametrize("kind, cols", [("IQ3_S", 4352), ("IQ3_S", 4608), ("IQ3_S", 8192), ("Q2_0", 6400),
+                                        ("Q2_0", 8192)])
+@pytest.mark.parametrize("tokens", [1, 4, 9])
+def test_window_matvec_of_wide_rows(kind, cols, tokens, tables, dev):
+    """Rows past 4096 columns: the streaming kernel where its waves split the row evenly and its ring fits in LDS,
+    the generic window kernel otherwise; the stack form refuses the rows it cannot split instead of dropping the
+    remainder (IQ3_S at 4352: 136 runs, not a multiple of the 16 a wave)."""
+    R = 48
+    raw, w = stack(kind, 1, R, cols, cols + tokens, tables)
+    rng = np.random.default_rng(cols + tokens)
+    x, xv = act(rng, (tokens, cols), "bfloat16")
+    got = SB.window_matvec(torch.from_numpy(raw).to(dev), kind, R, cols, x.to(dev)).float().cpu().numpy()
+    want = xv.astype(np.float64) @ w[0].T.astype(np.float64)
+    assert rel_err(got, want) <= TOL["bfloat16"]
+    if kind == "IQ3_S" and cols == 4352:
+        with pytest.raises(Exception, match="columns"):
+            SB.stack_matvec(torch.from_numpy(raw).to(dev), kind, (1, R, cols), x[None].to(dev))
+
+
+@pytest.mark.parametrize("dtype", ["bfloat16", "float16"])
+@pytest.mark.parametrize("tokens", [3, 4])
+@pytest.mark.parametrize("shape", [(40, 512, 1024), (12, 1536, 2048), (36, 528, 1024)])
+def test_q2_stacks_of_three_and_four_tokens(shape, tokens, dtype, tables, dev):
+    """Q2_0 stacks of many 32-row items at 3 and 4 tokens: the block-ring form whose waves each take both row groups
+    of an item over a quarter or an eighth of the columns (one set of activation registers for 32 rows), the other
+    column splits' sums added by the first split's wave; for 528 rows a matrix the last item has one row group."""
+    n, R, C = shape
+    raw, w = stack("Q2_0", n, R, C, 60 + tokens, tables)
+    rng = np.random.default_rng(70 + tokens)
+    x, xv = act(rng, (n, tokens, C), dtype)
+    got = SB.stack_matvec(torch.from_numpy(raw).to(dev), "Q2_0", (n, R, C), x.to(dev)).float().cpu().numpy()
+    want = np.stack([xv[m].astype(np.float64) @ w[m].T.astype(np.float64) for m in range(n)])
+    for m in (0, n // 2, n - 1):
+        assert rel_err(got[m], want[m]) <= TOL[dtype]
+    assert rel_err(got, want) <= TOL[dtype]
+
+
 @pytest.mark.parametrize("kind", ["Q2_0", "IQ3_S"])
 def test_window_matvec_bits_do_not_depend_on_the_window(kind, tables, dev):
     raw, w = stack(kind, 1, 96, 2048, 30, tables)

@@ -220,7 +220,7 @@ def test_block_linear_with_reordered_inputs(tables, dev):
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
-@pytest.mark.parametrize("tokens", [1, 3, 8, 24])
+@pytest.mark.parametrize("tokens", [1, 2, 3, 4, 5, 6, 7, 8, 24])
 def test_scaled_linear(dtype, tokens, dev):
     """Q6_K as codes, scales and d (dense.py:109-167): a window on the three parts, a chunk on the floats."""
     R, C = 192, 768

@@ -75,6 +75,48 @@ def test_float32_logits_route_exactly(tokens, tables, dev):
     assert rel_err(out.float().cpu(), want) <= 1e-2
 
 
+@pytest.mark.parametrize("E", [256, 1024, 2048])
+@pytest.mark.parametrize("tokens, logit_dtype", [(1, torch.bfloat16), (3, torch.float32), (9, torch.bfloat16)])
+def test_many_experts_route_exactly(E, tokens, logit_dtype, tables, dev):
+    """The route at 4, 16 and 32 keys a lane (256, 1024 and 2048 experts), with ties at the k-th value, through the
+    whole step at narrow widths (d 64, ffn 64: one Q2_0 block a row)."""
+    D, F, K = 64, 64, 12
+    lin, w, rng = layer("Q2_0", "Q2_0", E, D, F, E + tokens, dev, tables)
+    x = torch.from_numpy(rng.standard_normal((tokens, D)).astype(np.float32)).to(torch.bfloat16)
+    logits = torch.from_numpy(rng.standard_normal((tokens, E)).astype(np.float32)).to(logit_dtype)
+    top = torch.topk(logits.float(), K, dim=1).indices
+    logits[:, E - 1] = logits[torch.arange(tokens), top[:, K - 1]]  # the last expert ties with the k-th choice
+    wg = torch.from_numpy(rng.standard_normal(D).astype(np.float32) * 0.05).to(torch.bfloat16)
+    moe = SF.MoEDecode(lin["gate"], lin["up"], lin["down"], lin["sgate"], lin["sup"], lin["sdown"], wg.to(dev), K)
+    assert moe.takes(x)
+    out, idx, wt = moe(logits.to(dev), x.to(dev), want_choice=True)
+    want, want_idx, want_w = OM.moe_decode(logits.float().numpy(), x.float().numpy(), K,
+                                           (w["gate"], w["up"], w["down"]), (w["sgate"], w["sup"], w["sdown"]),
+                                           wg.float().numpy(), "bfloat16")
+    np.testing.assert_array_equal(idx.cpu().numpy(), want_idx)
+    np.testing.assert_allclose(wt.cpu().numpy(), want_w, rtol=2e-6, atol=1e-7)
+    assert rel_err(out.float().cpu(), want) <= 1e-2
+
+
+@pytest.mark.parametrize("kinds, D, F", [(("Q2_0", "Q2_0"), 320, 64), (("Q2_0", "Q2_0"), 576, 192),
+                                         (("Q2_0", "Q2_0"), 128, 320), (("IQ3_S", "Q2_0"), 768, 192)])
+@pytest.mark.parametrize("tokens", [1, 5])
+def test_widths_of_any_whole_blocks(kinds, D, F, tokens, tables, dev):
+    """Rows of a number of scale groups that four waves do not split evenly (5, 9 and 2 Q2_0 blocks of gate / up):
+    every group counted once."""
+    E, K = 64, 6
+    lin, w, rng = layer(*kinds, E, D, F, D + F + tokens, dev, tables)
+    x = torch.from_numpy(rng.standard_normal((tokens, D)).astype(np.float32)).to(torch.bfloat16)
+    logits = torch.from_numpy(rng.standard_normal((tokens, E)).astype(np.float32)).to(torch.bfloat16)
+    wg = torch.from_numpy(rng.standard_normal(D).astype(np.float32) * 0.05).to(torch.bfloat16)
+    moe = SF.MoEDecode(lin["gate"], lin["up"], lin["down"], lin["sgate"], lin["sup"], lin["sdown"], wg.to(dev), K)
+    assert moe.takes(x)
+    out = moe(logits.to(dev), x.to(dev))
+    want, _, _ = OM.moe_decode(logits.float().numpy(), x.float().numpy(), K, (w["gate"], w["up"], w["down"]),
+                               (w["sgate"], w["sup"], w["sdown"]), wg.float().numpy(), "bfloat16")
+    assert rel_err(out.float().cpu(), want) <= 1e-2
+
+
 def test_repeated_calls_reuse_the_workspace(tables, dev):
     """The down kernel's row-tile counters return to zero: call after call gives the same bits."""
     E, D, F, K = 64, 512, 256, 8

@@ -22,8 +22,9 @@ SELECTION = [
     ("test_gpu_attention.py", None),
     ("test_gpu_attention_entry.py", None),
     ("test_gpu_hc.py", None),
-    ("test_gpu_blocks.py", "dequantize or test_switch_matvec or separate or glu or lookup or window"),
-    ("test_gpu_moe.py", "test_moe_decode_is_the_oracles_block or float32_logits_route or repeated_calls"),
+    ("test_gpu_blocks.py", "dequantize or test_switch_matvec or separate or glu or lookup or window or three_and_four"),
+    ("test_gpu_moe.py", "test_moe_decode_is_the_oracles_block or float32_logits_route or repeated_calls or many_experts "
+                        "or whole_blocks"),
     ("test_gpu_tiles.py", "not 4096 and not skewed"),
     ("test_gpu_dropin.py", "not reference_models_shape and not install_routers"),
 ]
