@@ -105,11 +105,13 @@ static size_t moe_carve(MoeWs* ws, uint8_t* base, int64_t B, int64_t k, int64_t 
 // ---- route
 
 // Route keys: a logit in an order-preserving unsigned form above the complement of its index, so the largest key
-// is the largest logit and, among equal logits, the lowest index. 16-bit logits make 32-bit keys; float32 64-bit.
+// is the largest logit and, among equal logits, the lowest index (-0 taken as +0: equal, as float comparisons have
+// them). 16-bit logits make 32-bit keys; float32 64-bit.
 template <typename LT> struct RouteKey {
   using type = uint32_t;
   __device__ static __forceinline__ uint32_t make(LT v, int i) {
     uint32_t b = __builtin_bit_cast(uint16_t, v);
+    b = b == 0x8000u ? 0u : b;
     b = (b & 0x8000u) ? (~b & 0xffffu) : (b | 0x8000u);
     return (b << 16) | (0xffffu - (uint32_t)i);
   }
@@ -124,6 +126,7 @@ template <> struct RouteKey<float> {
   using type = uint64_t;
   __device__ static __forceinline__ uint64_t make(float v, int i) {
     uint32_t b = __float_as_uint(v);
+    b = b == 0x80000000u ? 0u : b;
     b = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
     return ((uint64_t)b << 32) | (0xffffffffu - (uint32_t)i);
   }

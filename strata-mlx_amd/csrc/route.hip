@@ -40,9 +40,11 @@ __global__ __launch_bounds__(256) void k_router_matvec(const WT* __restrict__ w,
 // (strata_mlx/fused.py:400-418), and optionally the softmax of the chosen logits (fused.py:491).
 //
 // One wave a row. A logit and its index make one 64-bit key that orders as (value, -index): the largest key is the
-// largest value and, among equal values, the lowest index. The wave's largest key is found on DPP (xmv.h).
+// largest value and, among equal values, the lowest index (-0 and +0 equal, as the reference's float comparisons
+// have them). The wave's largest key is found on DPP (xmv.h).
 __device__ __forceinline__ uint64_t topk_key(float v, int i) {
   uint32_t u = __float_as_uint(v);
+  u = u == 0x80000000u ? 0u : u;                     // -0 as +0
   u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);  // float order as unsigned order
   return ((uint64_t)u << 32) | (uint32_t)(0x7fffffff - i);
 }

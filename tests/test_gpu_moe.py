@@ -86,6 +86,11 @@ def test_many_experts_route_exactly(E, tokens, logit_dtype, tables, dev):
     logits = torch.from_numpy(rng.standard_normal((tokens, E)).astype(np.float32)).to(logit_dtype)
     top = torch.topk(logits.float(), K, dim=1).indices
     logits[:, E - 1] = logits[torch.arange(tokens), top[:, K - 1]]  # the last expert ties with the k-th choice
+    if tokens > 1:  # a token whose k-th choice falls among signed zeros: equal, chosen by index
+        logits[1] = -logits[1].abs() - 1
+        logits[1, :K - 2] = 1
+        logits[1, K - 2::3] = -0.0
+        logits[1, K - 1::3] = 0.0
     wg = torch.from_numpy(rng.standard_normal(D).astype(np.float32) * 0.05).to(torch.bfloat16)
     moe = SF.MoEDecode(lin["gate"], lin["up"], lin["down"], lin["sgate"], lin["sup"], lin["sdown"], wg.to(dev), K)
     assert moe.takes(x)

@@ -31,6 +31,23 @@ def test_top_k_is_the_oracles_choice(tokens, ties, dtype, dev):
         np.testing.assert_allclose(w.cpu().numpy(), OR.routing_weights(lt.float().numpy(), want), rtol=2e-6, atol=1e-7)
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+def test_top_k_takes_signed_zeros_as_equal(dtype, dev):
+    """-0 and +0 compare equal in the reference's choice (fused.py:400-418: float comparisons, ties to the lower
+    index): a row of signed zeros around the k-th place is chosen by index, not by sign."""
+    rng = np.random.default_rng(5)
+    logits = np.zeros((6, 96), dtype=np.float32)
+    logits[:, :4] = rng.uniform(1, 2, (6, 4))
+    logits[:, 40:] = -rng.uniform(1, 2, (6, 56))
+    logits[:, 4:40] = np.where(rng.random((6, 36)) < 0.5, -0.0, 0.0)
+    lt = torch.from_numpy(logits).to(dtype)
+    for k in (6, 10, 20):
+        idx, w = SF.top_k(lt.to(dev), k, weights=True)
+        want = OR.top_k(lt.float().numpy(), k)
+        np.testing.assert_array_equal(idx.cpu().numpy(), want)
+        np.testing.assert_array_equal(want[:, 4:k], np.tile(np.arange(4, k), (6, 1)))  # zeros by index
+
+
 @pytest.mark.parametrize("n, k", [(64, 1), (2048, 10), (96, 96), (100, 7)])
 def test_top_k_shapes(n, k, dev):
     rng = np.random.default_rng(n)

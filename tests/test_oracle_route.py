@@ -44,6 +44,8 @@ def test_top_k_special_rows():
     assert OR.top_k(neg, 3)[0].tolist() == [0, 1, 2]
     inf = np.array([[1.0, np.inf, -np.inf, 2.0]], np.float32)
     assert OR.top_k(inf, 4)[0].tolist() == [1, 3, 0, 2]
+    zeros = np.array([[-0.0, 1.0, 0.0, -0.0, -1.0, 0.0]], np.float32)
+    assert OR.top_k(zeros, 4)[0].tolist() == [1, 0, 2, 3]  # -0 and +0 equal (float comparisons): by index
 
 
 # ---- routing weights (fused.py:491: softmax of the chosen float32 logits)
