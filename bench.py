@@ -317,10 +317,11 @@ def matvec_stream(dev, steps, warmup):
 
 
 def matvec_sweep(dev, steps, warmup):
-    """C1 and C2's sweep: one 3072 x 2048 matvec a launch over distinct matrices (a stack past the Infinity Cache,
-    graph-captured launches): Q2_0 with float32 activations (x [1, 2048] float32, out float32: the exact path) and
-    every kind with bf16 activations at B = 1 (Q2_0 and IQ3_S by the MFMA stream, the others by the generic
-    kernels). Bytes a call: the matrix's blocks + x + out."""
+    """C1 and C2's sweep, 3072 x 2048 at B = 1 over distinct matrices (a stack past the Infinity Cache): Q2_0 with
+    float32 activations (x [1, 2048] float32, out float32: the exact path) and every kind with bf16 activations
+    (Q2_0 and IQ3_S by the MFMA kernels, the others, and float32, by the exact-weight stream). Two forms: one matrix
+    a launch (graph-captured launches: window_matvec as a layer calls it), and the whole stack in one launch
+    (stack_matvec: the streaming throughput). Bytes a matrix: its blocks + x + out."""
     import torch
 
     from strata_hip import blocks as SB
@@ -353,8 +354,26 @@ def matvec_sweep(dev, steps, warmup):
         key = f"{kind}_{'fp32' if dt == torch.float32 else 'bf16'}"
         res[key] = {"us": round(sec * 1e6, 2), "GBps": round(nbytes / sec / 1e9, 1),
                     "frac": round(nbytes / sec / 1e9 / HBM_PEAK_GBS, 4), "matrices": n}
+        del g
+        # the stack in one launch, each matrix its own vector
+        xs = torch.randn(n, 1, C, device=dev).to(dt)
+        SB.stack_matvec(blocks, kind, (n, R, C), xs)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            SB.stack_matvec(blocks, kind, (n, R, C), xs)
+        for _ in range(warmup):
+            g.replay()
+        torch.cuda.synchronize()
+        e0.record()
+        for _ in range(steps):
+            g.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        sec = e0.elapsed_time(e1) * 1e-3 / steps
+        res[key].update(stream_us=round(sec * 1e6, 1), stream_GBps=round(n * nbytes / sec / 1e9, 1),
+                        stream_frac=round(n * nbytes / sec / 1e9 / HBM_PEAK_GBS, 4))
         print(f"# C1/C2 sweep {key} B=1: {res[key]}", file=sys.stderr, flush=True)
-        del blocks, g
+        del blocks, g, xs
         torch.cuda.empty_cache()
     return res
 

@@ -12,19 +12,6 @@
 
 namespace sh {
 
-// x row of pair `pair` read by lanes: float32 dot of 32 weights with 32 activations
-template <typename XT> __device__ __forceinline__ float dot32(const float* w, const XT* x) {
-  float s = 0.0f;
-#pragma unroll
-  for (int j = 0; j < 32; ++j) s = fmaf(w[j], to_f32(x[j]), s);
-  return s;
-}
-
-__device__ __forceinline__ float lanes_sum(float v, int P) {
-  for (int o = P >> 1; o > 0; o >>= 1) v += __shfl_xor(v, o);
-  return v;
-}
-
 template <int KIND, typename OT>
 __global__ __launch_bounds__(256) void k_dequant(const uint8_t* __restrict__ blocks, const uint8_t* __restrict__ tabs,
                                                  OT* __restrict__ out, int64_t total_runs, int runs, int64_t rbytes) {
@@ -321,6 +308,9 @@ int sh_window_matvec(int kind, const void* blocks, const void* tables, int64_t r
   if (tokens <= 0) return OK;
   if (tokens > 8) return fail(E_SHAPE, "window_matvec: %lld tokens (a window is at most 8)", (long long)tokens);
   if (!blocks || !x || !out || (needs_tables(kind) && !tables)) return fail(E_ARG, "window_matvec: null pointer");
+  // the streaming kernel where it takes the layer (the same bits), else a block a few rows
+  st = stream_matvec(false, kind, blocks, tables, 1, rows, cols, x, x_dtype, tokens, out, stream);
+  if (st != E_UNSUPPORTED) return st;
   int P = lanes_per_row(cols / 32);
   return with_kind(kind, [&](auto kc) {
     constexpr int K = decltype(kc)::value;

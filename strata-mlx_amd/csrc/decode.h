@@ -186,6 +186,20 @@ template <> __device__ __forceinline__ void unpack32<IQ1_M>(const uint8_t* row, 
   }
 }
 
+// float32 dot of a run's 32 weights with 32 activations, in order (the generic kernels' sum of a run)
+template <typename XT> __device__ __forceinline__ float dot32(const float* w, const XT* x) {
+  float s = 0.0f;
+#pragma unroll
+  for (int j = 0; j < 32; ++j) s = fmaf(w[j], to_f32(x[j]), s);
+  return s;
+}
+
+// the sum over the P lanes (a power of two, an aligned group of a wave) that share a row, as a butterfly
+__device__ __forceinline__ float lanes_sum(float v, int P) {
+  for (int o = P >> 1; o > 0; o >>= 1) v += __shfl_xor(v, o);
+  return v;
+}
+
 // silu(g) * u as the reference rounds it: sigmoid in float32 rounded to the activations' type, then g * sigma
 // and * u each rounded to that type (strata_mlx/blocks.py:222-237).
 template <typename XT> __device__ __forceinline__ XT swiglu_one(XT g, XT u) {

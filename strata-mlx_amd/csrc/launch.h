@@ -99,4 +99,9 @@ inline void row_layout(int64_t rbytes, bool aligned, int& rstride, int& padded) 
   padded = 1;
 }
 
+// the streaming matvec of every kind (stream.hip): out[m][t] = W_m . x[m][t] for n_mats matrices and 1-8 tokens,
+// the generic kernels' arithmetic; E_UNSUPPORTED where it does not take the arguments (dry: checks and plan only)
+int stream_matvec(bool dry, int kind, const void* blocks, const void* tables, int64_t n_mats, int64_t rows,
+                  int64_t cols, const void* x, int x_dtype, int64_t tokens, void* out, void* stream);
+
 }  // namespace sh

@@ -522,9 +522,10 @@ static int stack_matvec(bool dry, int kind, const void* blocks, const void* tabl
   if (n_mats * ((rows + 15) / 16) > (1ll << 31) - 1 || rows * row_bytes(kind, cols) > (1ll << 31) - 1)
     return fail(E_SHAPE, "stack_matvec: %lld matrices of %lld x %lld too many", (long long)n_mats, (long long)rows,
                 (long long)cols);
+  // the other kinds, float32 activations and rows the MFMA decode does not tile: the streaming kernel of exact
+  // weights and float32 sums (stream.hip), which refuses what it does not take
   if (!mfma_kind_host(kind) || (x_dtype != BF16 && x_dtype != F16) || cols % 256)
-    return fail(E_UNSUPPORTED, "stack_matvec: kind %d, dtype %d, %lld columns (Q2_0 / IQ3_S, bf16 / fp16, columns a "
-                "multiple of 256)", kind, x_dtype, (long long)cols);
+    return stream_matvec(dry, kind, blocks, tables, n_mats, rows, cols, x, x_dtype, tokens, out, stream);
   if (!blocks || !x || (!out && !dry) || (kind == IQ3_S && !tables)) return fail(E_ARG, "stack_matvec: null pointer");
   if (((uintptr_t)x & 15) || (tables && ((uintptr_t)tables & 15)))
     return fail(E_ARG, "stack_matvec: activations and tables must be 16-byte aligned");

@@ -1,0 +1,218 @@
+// Streaming matvec of every block kind with float32 sums of exact weights: out[m][t] = W_m . x[m][t] for a stack
+// of n_mats matrices and up to 8 tokens each (one matrix is strata-mlx's window matvec, strata_mlx/blocks.py:
+// 351-394: a window of T <= 8 tokens, each run unpacked once for all of them). Serves float32 activations and the
+// kinds the MFMA kernels do not decode, for one layer (sh_window_matvec) and for a stack (sh_stack_matvec).
+//
+// Arithmetic: the generic kernels' own, bit for bit (blocks.hip k_window_matvec): P lanes share a row, lane `part`
+// takes the runs part, part + P, ... in order, each run's 32 weights decoded exactly (decode.h unpack32) and
+// dotted with the token's 32 activations in order, the P lanes' sums met by a butterfly. Only where the bytes come
+// from differs:
+//   - persistent blocks of 256 threads each take a contiguous run of items (tile_rows rows of one matrix); an
+//     item's bytes, contiguous in the stack, are read with 16-byte loads (all 256 threads, consecutive chunks:
+//     fully coalesced) into registers while the item before is multiplied, then written to LDS;
+//   - the activations of a block's current matrix sit in LDS as they are (the element type), a run of 32 at a
+//     stride padded by 16 bytes, so the lanes of a wave reading 64 different runs with 16-byte reads fall in
+//     distinct banks; each activation is read from LDS, never again from memory;
+//   - the kind's codebook tables are in LDS (static).
+#include <algorithm>
+#include <type_traits>
+
+#include "decode.h"
+#include "launch.h"
+
+namespace sh {
+
+constexpr int SM_NT = 256;                          // threads a block
+constexpr int SM_LOADS = 4;                         // 16-byte loads a thread an item, at most
+constexpr int SM_TILE = SM_LOADS * SM_NT * 16;      // LDS bytes of an item's buffer (16 KiB)
+constexpr int SM_X_MAX = 96 * 1024;                 // LDS bytes the activations of a matrix may take
+
+// one launch's shape, shared by host and device through the kernel arguments
+struct StreamPlan {
+  int rows, cols, tokens, runs, P, rp;  // rp = 256 / P rows a pass of the block
+  int64_t rbytes, mat_bytes;
+  int tile_rows, items_per_mat;
+  int64_t items, per;                   // items of the stack; a block's
+  int x_stride, x_bytes;                // LDS bytes a run of activations; of a matrix's activations
+  int loads;                            // 16-byte loads a thread an item
+};
+
+// float32 dot of a run's 32 weights with 32 activations read from LDS as 16-byte vectors (dot32's order)
+template <typename XT> __device__ __forceinline__ float dot32_lds(const float* w, const uint8_t* xr) {
+  constexpr int NV = 32 * (int)sizeof(XT) / 16;
+  u32x4 v[NV];
+#pragma unroll
+  for (int i = 0; i < NV; ++i) v[i] = *(const u32x4*)(xr + 16 * i);
+  return dot32<XT>(w, (const XT*)v);
+}
+
+template <int KIND, typename XT, int TM>
+__global__ __launch_bounds__(SM_NT) void k_stream_mv(const uint8_t* __restrict__ blocks, StreamPlan S,
+                                                     const XT* __restrict__ x, XT* __restrict__ out,
+                                                     const uint8_t* __restrict__ tabs) {
+  __shared__ u32x4 tab4[lds_tab_bytes(KIND) / 16];
+  extern __shared__ u32x4 dyn[];
+  uint8_t* tab = (uint8_t*)tab4;
+  uint8_t* xl = (uint8_t*)dyn;              // the current matrix's activations: [token][run], x_stride bytes a run
+  uint8_t* tl = (uint8_t*)dyn + S.x_bytes;  // the item's bytes from the 16-byte chunk holding its first
+  const int tid = threadIdx.x;
+  const int64_t first = (int64_t)blockIdx.x * S.per, last = min(S.items, first + S.per);
+  if (first >= last) return;  // the whole block
+  stage_tables<KIND>(tab, tabs);
+
+  // an item: rows [r0, r0 + nr) of matrix m, bytes [a, a + nr * rbytes) read from a16 = a rounded down to 16
+  // (inside the stack: the stack starts 16-byte aligned): `nfull` whole chunks by 16-byte loads, the `ntail`
+  // bytes after them one a thread
+  struct Span {
+    int64_t m;
+    int r0, nr, lead, nfull, ntail;
+    const uint8_t* a16;
+  };
+  auto span = [&](int64_t item) {
+    Span s;
+    s.m = item / S.items_per_mat;
+    s.r0 = (int)(item - s.m * S.items_per_mat) * S.tile_rows;
+    s.nr = min(S.tile_rows, S.rows - s.r0);
+    const int64_t off = s.m * S.mat_bytes + (int64_t)s.r0 * S.rbytes;
+    s.a16 = blocks + (off & ~(int64_t)15);  // from the kernel argument: global loads
+    s.lead = (int)(off & 15);
+    const int n = s.lead + s.nr * (int)S.rbytes;
+    s.nfull = n >> 4;
+    s.ntail = n & 15;
+    return s;
+  };
+  u32x4 stg[SM_LOADS];
+  uint32_t stail = 0;
+  auto issue = [&](const Span& s) {
+#pragma unroll
+    for (int j = 0; j < SM_LOADS; ++j) {
+      const int c = j * SM_NT + tid;
+      if (j < S.loads && c < s.nfull) stg[j] = *(const u32x4*)(s.a16 + 16 * c);
+    }
+    if (tid < s.ntail) stail = s.a16[16 * s.nfull + tid];
+  };
+  auto commit = [&](const Span& s) {
+#pragma unroll
+    for (int j = 0; j < SM_LOADS; ++j) {
+      const int c = j * SM_NT + tid;
+      if (j < S.loads && c < s.nfull) *(u32x4*)(tl + 16 * c) = stg[j];
+    }
+    if (tid < s.ntail) tl[16 * s.nfull + tid] = (uint8_t)stail;
+  };
+  // matrix m's activations into LDS: x[m] is [tokens][cols], so 16-byte vector v lies in run (t * runs + n)
+  auto stage_x = [&](int64_t m) {
+    constexpr int RB = 32 * (int)sizeof(XT);
+    const uint8_t* xs = (const uint8_t*)(x + m * S.tokens * S.cols);
+    const int nv = S.tokens * S.cols * (int)sizeof(XT) / 16;
+    for (int v = tid; v < nv; v += SM_NT) {
+      const int tr = (16 * v) / RB, o = 16 * v - tr * RB;
+      *(u32x4*)(xl + tr * S.x_stride + o) = *(const u32x4*)(xs + 16 * v);
+    }
+  };
+
+  const int part = tid & (S.P - 1), rin = tid / S.P;
+  int64_t cur = -1;
+  issue(span(first));
+  for (int64_t item = first; item < last; ++item) {
+    const Span s = span(item);
+    __syncthreads();  // every wave is done with the item before (and with its activations)
+    commit(s);
+    if (s.m != cur) {
+      stage_x(s.m);
+      cur = s.m;
+    }
+    if (item + 1 < last) issue(span(item + 1));  // in flight while this item is multiplied
+    __syncthreads();
+    for (int r = rin; r < s.nr; r += S.rp) {  // the P lanes of a row leave together
+      const uint8_t* row = tl + s.lead + (int64_t)r * S.rbytes;
+      float w[32], sum[TM];
+#pragma unroll
+      for (int t = 0; t < TM; ++t) sum[t] = 0.0f;
+      for (int n = part; n < S.runs; n += S.P) {
+        unpack32<KIND>(row, n, w, tab);
+#pragma unroll
+        for (int t = 0; t < TM; ++t)
+          if (t < S.tokens) sum[t] += dot32_lds<XT>(w, xl + (t * S.runs + n) * S.x_stride);
+      }
+#pragma unroll
+      for (int t = 0; t < TM; ++t) {
+        if (t < S.tokens) {
+          const float total = lanes_sum(sum[t], S.P);
+          if (part == 0) out[(s.m * S.tokens + t) * S.rows + s.r0 + r] = from_f32<XT>(total);
+        }
+      }
+    }
+  }
+}
+
+// The plan for n_mats matrices of rows x cols of `kind` and `tokens` activations of `x_dtype`; E_UNSUPPORTED where
+// the kernel does not take them (the callers then take another kernel or refuse).
+static int stream_plan(int kind, int x_dtype, const void* blocks, const void* x, int64_t n_mats, int64_t rows,
+                       int64_t cols, int64_t tokens, StreamPlan& S) {
+  if (tokens < 1 || tokens > 8) return fail(E_UNSUPPORTED, "stream matvec: %lld tokens (1 to 8)", (long long)tokens);
+  if (((uintptr_t)blocks & 15) || ((uintptr_t)x & 15))
+    return fail(E_UNSUPPORTED, "stream matvec: blocks and activations must be 16-byte aligned");
+  const int64_t runs = cols / 32, rb = row_bytes(kind, cols), xs = 32 * dtype_size(x_dtype) + 16;
+  if (tokens * runs * xs > SM_X_MAX)
+    return fail(E_UNSUPPORTED, "stream matvec: %lld tokens of %lld activations do not fit LDS", (long long)tokens,
+                (long long)cols);
+  const int P = lanes_per_row(runs), rp = SM_NT / P;
+  const int64_t fit = (SM_TILE - 32) / rb / rp * rp;  // rows an item's buffer holds, whole passes
+  if (fit < rp) return fail(E_UNSUPPORTED, "stream matvec: rows of %lld bytes too long", (long long)rb);
+  if (n_mats * rows * rb > (1ll << 62) || rows > (1 << 30))
+    return fail(E_SHAPE, "stream matvec: stack too large");
+  // items small enough that a single matrix spreads over the CUs twice, at most what the buffer holds
+  const int64_t want = std::max<int64_t>(rp, n_mats * rows / (2 * device_cus()) / rp * rp);
+  S.rows = (int)rows, S.cols = (int)cols, S.tokens = (int)tokens, S.runs = (int)runs, S.P = P, S.rp = rp;
+  S.rbytes = rb, S.mat_bytes = rows * rb;
+  S.tile_rows = (int)std::min(fit, want);
+  S.items_per_mat = (int)((rows + S.tile_rows - 1) / S.tile_rows);
+  S.items = n_mats * S.items_per_mat;
+  S.x_stride = (int)xs, S.x_bytes = (int)(tokens * runs * xs);
+  const int64_t nmax = (15 + (int64_t)S.tile_rows * rb) / 16;  // whole chunks of an item, at most
+  S.loads = (int)((nmax + SM_NT - 1) / SM_NT);
+  return OK;
+}
+
+template <int KIND, typename XT, int TM>
+static int launch_stream(const StreamPlan& S0, const uint8_t* blocks, const uint8_t* tabs, const XT* x, XT* out,
+                         hipStream_t stream, bool dry) {
+  StreamPlan S = S0;
+  auto kern = k_stream_mv<KIND, XT, TM>;
+  const size_t dyn_lds = (size_t)S.x_bytes + SM_TILE;
+  const size_t lds = dyn_lds + static_lds(kern);
+  if (lds > LDS_BYTES) return fail(E_UNSUPPORTED, "stream matvec: %zu bytes of LDS", lds);
+  if (dry) return OK;
+  const int64_t bpc = std::max<int64_t>(1, std::min<int64_t>(8, (int64_t)LDS_BYTES / (int64_t)lds));
+  const int64_t cap = (int64_t)device_cus() * bpc;
+  S.per = (S.items + cap - 1) / cap;
+  const int64_t grid = (S.items + S.per - 1) / S.per;
+  hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(SM_NT), dyn_lds, stream, blocks, S, x, out, tabs);
+  return check_launch("stream matvec");
+}
+
+// the streaming matvec's checks, plan and launch (dry: checks and plan only); E_UNSUPPORTED where it does not take
+// the arguments
+int stream_matvec(bool dry, int kind, const void* blocks, const void* tables, int64_t n_mats, int64_t rows,
+                  int64_t cols, const void* x, int x_dtype, int64_t tokens, void* out, void* stream) {
+  int st = check_rows(kind, rows, cols, "stream matvec");
+  if (st) return st;
+  if (!blocks || !x || (!out && !dry) || (needs_tables(kind) && !tables))
+    return fail(E_ARG, "stream matvec: null pointer");
+  StreamPlan S;
+  st = stream_plan(kind, x_dtype, blocks, x, n_mats, rows, cols, tokens, S);
+  if (st) return st;
+  return with_kind(kind, [&](auto kc) {
+    constexpr int K = decltype(kc)::value;
+    return with_dtype(x_dtype, [&](auto* tp) {
+      using XT = std::remove_pointer_t<decltype(tp)>;
+      if (tokens == 1)
+        return launch_stream<K, XT, 1>(S, (const uint8_t*)blocks, (const uint8_t*)tables, (const XT*)x, (XT*)out,
+                                       (hipStream_t)stream, dry);
+      return launch_stream<K, XT, 8>(S, (const uint8_t*)blocks, (const uint8_t*)tables, (const XT*)x, (XT*)out,
+                                     (hipStream_t)stream, dry);
+    });
+  });
+}
+
+}  // namespace sh

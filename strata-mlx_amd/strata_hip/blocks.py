@@ -151,12 +151,13 @@ def stack_takes(kind: str, cols: int, dtype: torch.dtype) -> bool:
 
 
 def stack_matvec(blocks: torch.Tensor, kind: str, shape: tuple, x: torch.Tensor) -> torch.Tensor:
-    """out[m, t] = W_m . x[m, t] for a stack of `shape` (matrices, rows, cols) and x (matrices, tokens <= 16, cols)
-    bf16 / fp16: the window matvec (strata_mlx/blocks.py:351-394) over many matrices in one launch, streaming their
-    blocks. Returns (matrices, tokens, rows) in x's type."""
+    """out[m, t] = W_m . x[m, t] for a stack of `shape` (matrices, rows, cols) and x (matrices, tokens, cols): the
+    window matvec (strata_mlx/blocks.py:351-394) over many matrices in one launch, streaming their blocks. Returns
+    (matrices, tokens, rows) in x's type. Q2_0 / IQ3_S with bf16 / fp16 activations (rows of whole 256s) take the
+    MFMA kernels, up to 16 tokens; every other kind, and float32 activations, the exact-weight kernel (float32
+    sums, the generic window kernel's bits), up to 8 tokens."""
     n, rows, cols = shape
-    if not stack_takes(kind, cols, x.dtype):
-        raise ValueError(f"stack_matvec: {kind}, {cols} columns, {x.dtype} (Q2_0 / IQ3_S, cols % 256, bf16 / fp16)")
+    _check_cols(kind, cols)
     x = x.reshape(n, -1, cols).contiguous()
     tokens = x.shape[1]
     if blocks.numel() < n * rows * row_bytes(kind, cols):

@@ -1,0 +1,142 @@
+"""The streaming matvec of exact weights (every kind, float32 / bf16 / fp16 activations, one layer or a stack of
+matrices): the oracle's products within the path's tolerances, and the generic expert kernel's bits exactly (the
+same runs a lane, the same order of sums), a token's bits whatever its window."""
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import rel_err
+from oracle import blocks as OB
+from strata_hip import blocks as SB
+from strata_hip import synth
+
+pytestmark = pytest.mark.gpu
+
+KINDS = sorted(SB.BLOCK)
+TORCH = {"float32": torch.float32, "float16": torch.float16, "bfloat16": torch.bfloat16}
+TOL = {"float32": 1e-5, "float16": 1e-2, "bfloat16": 1e-2}
+
+
+def mats(kind, n, rows, cols, seed, tables):
+    rng = np.random.default_rng(seed)
+    raw = synth.random_blocks(kind, n * rows, cols, rng)
+    return raw, OB.dequantize(raw, kind, (n, rows, cols), tables)
+
+
+def act(rng, shape, dtype):
+    t = torch.from_numpy(rng.standard_normal(shape).astype(np.float32)).to(TORCH[dtype])
+    return t, t.float().numpy()
+
+
+def streamed(kind, dtype):
+    """Whether window_matvec takes the exact-weight stream (not the MFMA kernels) for this kind and dtype."""
+    return not (kind in ("Q2_0", "IQ3_S") and dtype != "float32")
+
+
+def generic(b, kind, shape, x, dev):
+    """The generic expert kernel, pair t = matrix m's token t: the reference bits of the stream."""
+    n, rows, cols = shape
+    tokens = x.shape[-2]
+    idx = torch.arange(n, dtype=torch.int32).repeat_interleave(tokens)
+    return SB.switch_matvec(b, kind, shape, idx.to(dev), x.reshape(-1, cols), 1).reshape(n, tokens, rows)
+
+
+@pytest.mark.parametrize("kind", KINDS)
+@pytest.mark.parametrize("dtype", ["float32", "bfloat16", "float16"])
+@pytest.mark.parametrize("tokens", [1, 3, 8])
+def test_window_matvec_of_every_kind(kind, dtype, tokens, tables, dev):
+    R, C = 200, 512  # rows not a multiple of an item's
+    raw, w = mats(kind, 1, R, C, 300 + tokens, tables)
+    rng = np.random.default_rng(310 + tokens)
+    x, xv = act(rng, (tokens, C), dtype)
+    b = torch.from_numpy(raw).to(dev)
+    got = SB.window_matvec(b, kind, R, C, x.to(dev)).cpu()
+    want = xv.astype(np.float64) @ w[0].T.astype(np.float64)
+    assert got.shape == (tokens, R) and got.dtype == TORCH[dtype]
+    assert rel_err(got.float().numpy(), want) <= TOL[dtype]
+    if streamed(kind, dtype):
+        assert torch.equal(got, generic(b, kind, (1, R, C), x[None].to(dev), dev)[0].cpu())
+
+
+@pytest.mark.parametrize("kind", KINDS)
+@pytest.mark.parametrize("dtype", ["float32", "bfloat16"])
+@pytest.mark.parametrize("tokens", [1, 5])
+def test_stack_matvec_of_every_kind(kind, dtype, tokens, tables, dev):
+    """Many matrices in one launch: items crossing from one matrix to the next, each matrix its own tokens."""
+    n, R, C = 6, 72, 1024
+    raw, w = mats(kind, n, R, C, 320 + tokens, tables)
+    rng = np.random.default_rng(330 + tokens)
+    x, xv = act(rng, (n, tokens, C), dtype)
+    b = torch.from_numpy(raw).to(dev)
+    got = SB.stack_matvec(b, kind, (n, R, C), x.to(dev)).cpu()
+    want = np.einsum("mrc,mtc->mtr", w.astype(np.float64), xv.astype(np.float64))
+    assert got.shape == (n, tokens, R)
+    assert rel_err(got.float().numpy(), want) <= TOL[dtype]
+    for m in (0, n - 1):
+        assert rel_err(got[m].float().numpy(), want[m]) <= TOL[dtype]
+    if streamed(kind, dtype):
+        assert torch.equal(got, generic(b, kind, (n, R, C), x.to(dev), dev).cpu())
+
+
+@pytest.mark.parametrize("kind, cols", [("Q2_0", 192), ("Q2_0", 2880), ("IQ4_NL", 96), ("Q3_K", 2560),
+                                        ("IQ1_M", 768), ("IQ2_XXS", 1280)])
+@pytest.mark.parametrize("tokens", [1, 2])
+def test_rows_not_whole_chunks(kind, cols, tokens, tables, dev):
+    """Rows whose bytes are not whole 16-byte chunks (Q2_0 at 54 and 810 bytes, IQ4_NL at 54, Q3_K at the reference
+    model's d 2560: 1,100): items start inside a chunk and end with loose bytes; rows of fewer runs than a wave."""
+    n, R = 3, 37
+    raw, w = mats(kind, n, R, cols, cols + tokens, tables)
+    rng = np.random.default_rng(cols + 7 * tokens)
+    x, xv = act(rng, (n, tokens, cols), "float32")
+    b = torch.from_numpy(raw).to(dev)
+    got = SB.stack_matvec(b, kind, (n, R, cols), x.to(dev)).cpu()
+    want = np.einsum("mrc,mtc->mtr", w.astype(np.float64), xv.astype(np.float64))
+    assert rel_err(got.numpy(), want) <= TOL["float32"]
+    assert torch.equal(got, generic(b, kind, (n, R, cols), x.to(dev), dev).cpu())
+    one = SB.window_matvec(b[: R * SB.row_bytes(kind, cols)], kind, R, cols, x[0].to(dev)).cpu()
+    assert torch.equal(one, got[0])
+
+
+@pytest.mark.parametrize("kind", ["Q2_0", "IQ4_XS", "IQ2_S"])
+def test_a_tokens_bits_do_not_depend_on_its_window(kind, tables, dev):
+    R, C = 96, 2048
+    raw, _ = mats(kind, 1, R, C, 340, tables)
+    x = torch.randn(8, C)
+    b = torch.from_numpy(raw).to(dev)
+    whole = SB.window_matvec(b, kind, R, C, x.to(dev)).cpu()
+    for t in (0, 3, 7):
+        assert torch.equal(SB.window_matvec(b, kind, R, C, x[t : t + 1].to(dev)).cpu()[0], whole[t])
+        assert torch.equal(SB.window_matvec(b, kind, R, C, x[: t + 1].to(dev)).cpu()[t], whole[t])
+
+
+def test_the_float32_matvec_at_its_benchmark_shape(tables, dev):
+    """Q2_0 3072 x 2048 with a float32 vector, out float32: 1e-5 of the oracle, the generic kernel's bits; and the
+    same matrix as one of a stack of eight."""
+    R, C, n = 3072, 2048, 8
+    raw, w = mats("Q2_0", n, R, C, 350, tables)
+    rng = np.random.default_rng(351)
+    x, xv = act(rng, (n, 1, C), "float32")
+    b = torch.from_numpy(raw).to(dev)
+    got = SB.window_matvec(b[: R * SB.row_bytes("Q2_0", C)], "Q2_0", R, C, x[0].to(dev)).cpu()
+    assert rel_err(got[0].numpy(), w[0].astype(np.float64) @ xv[0, 0].astype(np.float64)) <= 1e-5
+    assert torch.equal(got, generic(b, "Q2_0", (1, R, C), x[:1].to(dev), dev)[0].cpu())
+    stacked = SB.stack_matvec(b, "Q2_0", (n, R, C), x.to(dev)).cpu()
+    assert torch.equal(stacked[0], got)
+    want = np.einsum("mrc,mtc->mtr", w.astype(np.float64), xv.astype(np.float64))
+    assert rel_err(stacked.numpy(), want) <= 1e-5
+
+
+def test_the_stream_refuses_what_it_does_not_take(tables, dev):
+    """More than 8 tokens a matrix of an exact-weight kind, and activations too wide for LDS, are refused (the
+    MFMA kinds take 16 tokens in bf16 / fp16)."""
+    raw, _ = mats("IQ4_XS", 2, 16, 512, 360, tables)
+    b = torch.from_numpy(raw).to(dev)
+    with pytest.raises(Exception, match="tokens"):
+        SB.stack_matvec(b, "IQ4_XS", (2, 16, 512), torch.zeros((2, 9, 512), dtype=torch.bfloat16).to(dev))
+    wide = torch.from_numpy(mats("IQ4_NL", 1, 4, 4096, 361, tables)[0]).to(dev)
+    with pytest.raises(Exception, match="LDS"):
+        SB.stack_matvec(wide, "IQ4_NL", (1, 4, 4096), torch.zeros((1, 8, 4096)).to(dev))
+    # one layer of them still multiplies, through the generic window kernel
+    got = SB.window_matvec(wide, "IQ4_NL", 4, 4096, torch.ones((8, 4096)).to(dev))
+    assert got.shape == (8, 4)
