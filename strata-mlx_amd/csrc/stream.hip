@@ -37,6 +37,29 @@ struct StreamPlan {
   int loads;                            // 16-byte loads a thread an item
 };
 
+// A run's 32 weights for the dot products: unpack32's values, except that a zero weight may be +0 where unpack32
+// gives -0. The dot's float32 sums start at +0 and so are never -0, and adding a zero of either sign to them gives
+// the same value: the sums are unpack32's bits. Q2_0: d (q - 1) as fmaf(d, q, -d) (exact: d is a half, q - 1 in
+// -1..2), the codes of four bytes at once (one mask a code position, then a byte-to-float conversion a weight).
+template <int KIND> __device__ __forceinline__ void unpack32_dot(const uint8_t* row, int n, float* w, const uint8_t* tab) {
+  unpack32<KIND>(row, n, w, tab);
+}
+template <> __device__ __forceinline__ void unpack32_dot<Q2_0>(const uint8_t* row, int n, float* w, const uint8_t*) {
+  const uint8_t* b = row + (n >> 1) * 18;
+  const uint8_t* q = b + 2 + 8 * (n & 1);
+  const float d = half_at(b), nd = -d;
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const uint32_t c = rd32(q + 4 * h);  // code bytes 4h .. 4h + 3: weight 4i + j is byte i's bits 2j, 2j + 1
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint32_t m = (c >> (2 * j)) & 0x03030303u;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) w[4 * (4 * h + i) + j] = fmaf(d, (float)((m >> (8 * i)) & 0xffu), nd);
+    }
+  }
+}
+
 // float32 dot of a run's 32 weights with 32 activations read from LDS as 16-byte vectors (dot32's order)
 template <typename XT> __device__ __forceinline__ float dot32_lds(const float* w, const uint8_t* xr) {
   constexpr int NV = 32 * (int)sizeof(XT) / 16;
@@ -129,7 +152,7 @@ __global__ __launch_bounds__(SM_NT) void k_stream_mv(const uint8_t* __restrict__
 #pragma unroll
       for (int t = 0; t < TM; ++t) sum[t] = 0.0f;
       for (int n = part; n < S.runs; n += S.P) {
-        unpack32<KIND>(row, n, w, tab);
+        unpack32_dot<KIND>(row, n, w, tab);
 #pragma unroll
         for (int t = 0; t < TM; ++t)
           if (t < S.tokens) sum[t] += dot32_lds<XT>(w, xl + (t * S.runs + n) * S.x_stride);
