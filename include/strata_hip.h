@@ -78,8 +78,9 @@ int sh_switch_matvec_generic(int kind, const void* blocks, const void* const* ex
 /* strata_mlx/blocks.py:351-394 (window_matvec) over a stack: out[m][t] = W_m . x[m][t], x (n_mats, tokens, cols),
  * out (n_mats, tokens, rows) in x's type. Q2_0 or IQ3_S with bf16 / fp16 activations, cols a multiple of 256 up
  * to 4096 (wider rows where the waves' column splits and the LDS ring allow: sh_stack_takes says), up to 16 tokens:
- * the MFMA kernels. Every other kind, and float32 activations: the exact-weight stream (float32 sums, the bits of
- * sh_switch_matvec_generic), up to 8 tokens whose activations fit 96 KiB of LDS, blocks and x 16-byte aligned.
+ * the MFMA kernels. Every other kind, and float32 activations: the exact-weight stream (float32 sums; the bits of
+ * sh_switch_matvec_generic but for Q2_0, taken a run at a time as d (sum q x - sum x)), up to 8 tokens whose
+ * activations fit 96 KiB of LDS, blocks and x 16-byte aligned.
  * One streaming launch over all matrices (one per window of row tiles for the longest Q2_0 stacks).
  * workspace: sh_stack_workspace() bytes (none). */
 size_t sh_stack_workspace(int kind, int64_t n_mats, int64_t rows, int64_t cols, int64_t tokens, int x_dtype);
@@ -98,7 +99,8 @@ int sh_matvec_separate(int kind, const void* const* expert_ptrs, const void* tab
                        int64_t pairs, const void* x, int x_dtype, int64_t share, void* out, void* stream);
 
 /* strata_mlx/blocks.py:351-394 (window_matvec): out[t] = W . x[t], one layer, tokens <= 8; exact weights and
- * float32 sums (the exact-weight stream where it takes the layer, else a block a few rows: the same bits). */
+ * float32 sums (the exact-weight stream where it takes the layer, the bits of sh_stack_matvec's; else a block a few
+ * rows). */
 int sh_window_matvec(int kind, const void* blocks, const void* tables, int64_t rows, int64_t cols, const void* x,
                      int x_dtype, int64_t tokens, void* out, void* stream);
 

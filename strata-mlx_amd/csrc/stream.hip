@@ -3,10 +3,12 @@
 // 351-394: a window of T <= 8 tokens, each run unpacked once for all of them). Serves float32 activations and the
 // kinds the MFMA kernels do not decode, for one layer (sh_window_matvec) and for a stack (sh_stack_matvec).
 //
-// Arithmetic: the generic kernels' own, bit for bit (blocks.hip k_window_matvec): P lanes share a row, lane `part`
-// takes the runs part, part + P, ... in order, each run's 32 weights decoded exactly (decode.h unpack32) and
-// dotted with the token's 32 activations in order, the P lanes' sums met by a butterfly. Only where the bytes come
-// from differs:
+// Arithmetic: the generic kernels' own (blocks.hip k_window_matvec): P lanes share a row, lane `part` takes the
+// runs part, part + P, ... in order, each run's 32 weights decoded exactly (decode.h unpack32) and dotted with the
+// token's 32 activations in order, the P lanes' sums met by a butterfly: their bits, for every kind but Q2_0. A
+// Q2_0 run is taken as d (sum q x - sum x) (q the codes 0..3, sum x the run's activations summed once a matrix):
+// two VALU instructions a weight and a token (a conversion and an FMA) instead of four, different roundings (of
+// the same size). Where the bytes come from differs too:
 //   - persistent blocks of 256 threads each take a contiguous run of items (tile_rows rows of one matrix); an
 //     item's bytes, contiguous in the stack, are read with 16-byte loads (all 256 threads, consecutive chunks:
 //     fully coalesced) into registers while the item before is multiplied, then written to LDS;
@@ -33,29 +35,23 @@ struct StreamPlan {
   int64_t rbytes, mat_bytes;
   int tile_rows, items_per_mat;
   int64_t items, per;                   // items of the stack; a block's
-  int x_stride, x_bytes;                // LDS bytes a run of activations; of a matrix's activations
+  int x_stride, x_bytes, xsum_bytes;    // LDS bytes a run of activations; of a matrix's; of its runs' sums
   int loads;                            // 16-byte loads a thread an item
 };
 
-// A run's 32 weights for the dot products: unpack32's values, except that a zero weight may be +0 where unpack32
-// gives -0. The dot's float32 sums start at +0 and so are never -0, and adding a zero of either sign to them gives
-// the same value: the sums are unpack32's bits. Q2_0: d (q - 1) as fmaf(d, q, -d) (exact: d is a half, q - 1 in
-// -1..2), the codes of four bytes at once (one mask a code position, then a byte-to-float conversion a weight).
-template <int KIND> __device__ __forceinline__ void unpack32_dot(const uint8_t* row, int n, float* w, const uint8_t* tab) {
-  unpack32<KIND>(row, n, w, tab);
-}
-template <> __device__ __forceinline__ void unpack32_dot<Q2_0>(const uint8_t* row, int n, float* w, const uint8_t*) {
-  const uint8_t* b = row + (n >> 1) * 18;
-  const uint8_t* q = b + 2 + 8 * (n & 1);
-  const float d = half_at(b), nd = -d;
+// Q2_0's code values (0..3) of a run as floats, in weight order: weight 4i + j is bits 2j, 2j + 1 of code byte i.
+// Four bytes are masked at once a code position and each byte converted as it stands (the empty statement keeps
+// the compiler from folding mask and byte into a bit-field extract a weight).
+__device__ __forceinline__ void q2_codes(const uint8_t* q, float* c) {
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
-    const uint32_t c = rd32(q + 4 * h);  // code bytes 4h .. 4h + 3: weight 4i + j is byte i's bits 2j, 2j + 1
+    const uint32_t word = rd32(q + 4 * h);
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      const uint32_t m = (c >> (2 * j)) & 0x03030303u;
+      uint32_t m = (word >> (2 * j)) & 0x03030303u;
+      asm("" : "+v"(m));
 #pragma unroll
-      for (int i = 0; i < 4; ++i) w[4 * (4 * h + i) + j] = fmaf(d, (float)((m >> (8 * i)) & 0xffu), nd);
+      for (int i = 0; i < 4; ++i) c[4 * (4 * h + i) + j] = (float)((m >> (8 * i)) & 0xffu);
     }
   }
 }
@@ -77,7 +73,8 @@ __global__ __launch_bounds__(SM_NT) void k_stream_mv(const uint8_t* __restrict__
   extern __shared__ u32x4 dyn[];
   uint8_t* tab = (uint8_t*)tab4;
   uint8_t* xl = (uint8_t*)dyn;              // the current matrix's activations: [token][run], x_stride bytes a run
-  uint8_t* tl = (uint8_t*)dyn + S.x_bytes;  // the item's bytes from the 16-byte chunk holding its first
+  float* xsum = (float*)((uint8_t*)dyn + S.x_bytes);  // Q2_0: each run's sum of activations [token][run]
+  uint8_t* tl = (uint8_t*)dyn + S.x_bytes + S.xsum_bytes;  // the item's bytes from the 16-byte chunk holding its first
   const int tid = threadIdx.x;
   const int64_t first = (int64_t)blockIdx.x * S.per, last = min(S.items, first + S.per);
   if (first >= last) return;  // the whole block
@@ -127,9 +124,27 @@ __global__ __launch_bounds__(SM_NT) void k_stream_mv(const uint8_t* __restrict__
     constexpr int RB = 32 * (int)sizeof(XT);
     const uint8_t* xs = (const uint8_t*)(x + m * S.tokens * S.cols);
     const int nv = S.tokens * S.cols * (int)sizeof(XT) / 16;
-    for (int v = tid; v < nv; v += SM_NT) {
+    for (int v0 = 0; v0 < nv; v0 += SM_NT) {  // every lane the same rounds (the sums' lane exchanges)
+      const int v = v0 + tid;
+      const bool in = v < nv;
       const int tr = (16 * v) / RB, o = 16 * v - tr * RB;
-      *(u32x4*)(xl + tr * S.x_stride + o) = *(const u32x4*)(xs + 16 * v);
+      u32x4 xv = {0u, 0u, 0u, 0u};
+      if (in) {
+        xv = *(const u32x4*)(xs + 16 * v);
+        *(u32x4*)(xl + tr * S.x_stride + o) = xv;
+      }
+      if constexpr (KIND == Q2_0) {
+        // the run's sum: each lane its vector's elements in order, then the RB / 16 lanes of the run (consecutive,
+        // an aligned group: nv is whole runs) by a butterfly
+        constexpr int NE = 16 / (int)sizeof(XT), NL = RB / 16;
+        const XT* e = (const XT*)&xv;
+        float p = 0.0f;
+#pragma unroll
+        for (int i = 0; i < NE; ++i) p += to_f32(e[i]);
+#pragma unroll
+        for (int o2 = NL / 2; o2 > 0; o2 >>= 1) p += __shfl_xor(p, o2);
+        if (in && o == 0) xsum[tr] = p;
+      }
     }
   };
 
@@ -146,22 +161,34 @@ __global__ __launch_bounds__(SM_NT) void k_stream_mv(const uint8_t* __restrict__
     }
     if (item + 1 < last) issue(span(item + 1));  // in flight while this item is multiplied
     __syncthreads();
-    for (int r = rin; r < s.nr; r += S.rp) {  // the P lanes of a row leave together
+    for (int r0 = 0; r0 < s.nr; r0 += S.rp) {  // passes: every lane the same (the sums' lane exchanges)
+      const int r = r0 + rin;
+      const bool act = r < s.nr;  // the P lanes of a row alike
       const uint8_t* row = tl + s.lead + (int64_t)r * S.rbytes;
       float w[32], sum[TM];
 #pragma unroll
       for (int t = 0; t < TM; ++t) sum[t] = 0.0f;
-      for (int n = part; n < S.runs; n += S.P) {
-        unpack32_dot<KIND>(row, n, w, tab);
+      for (int n = act ? part : S.runs; n < S.runs; n += S.P) {
+        if constexpr (KIND == Q2_0) {  // d (sum q x - sum x): the scale and the offset once a run
+          const uint8_t* b = row + (n >> 1) * 18;
+          const float d = half_at(b);
+          q2_codes(b + 2 + 8 * (n & 1), w);
 #pragma unroll
-        for (int t = 0; t < TM; ++t)
-          if (t < S.tokens) sum[t] += dot32_lds<XT>(w, xl + (t * S.runs + n) * S.x_stride);
+          for (int t = 0; t < TM; ++t)
+            if (t < S.tokens)
+              sum[t] += d * (dot32_lds<XT>(w, xl + (t * S.runs + n) * S.x_stride) - xsum[t * S.runs + n]);
+        } else {
+          unpack32<KIND>(row, n, w, tab);
+#pragma unroll
+          for (int t = 0; t < TM; ++t)
+            if (t < S.tokens) sum[t] += dot32_lds<XT>(w, xl + (t * S.runs + n) * S.x_stride);
+        }
       }
 #pragma unroll
       for (int t = 0; t < TM; ++t) {
         if (t < S.tokens) {
           const float total = lanes_sum(sum[t], S.P);
-          if (part == 0) out[(s.m * S.tokens + t) * S.rows + s.r0 + r] = from_f32<XT>(total);
+          if (act && part == 0) out[(s.m * S.tokens + t) * S.rows + s.r0 + r] = from_f32<XT>(total);
         }
       }
     }
@@ -192,6 +219,7 @@ static int stream_plan(int kind, int x_dtype, const void* blocks, const void* x,
   S.items_per_mat = (int)((rows + S.tile_rows - 1) / S.tile_rows);
   S.items = n_mats * S.items_per_mat;
   S.x_stride = (int)xs, S.x_bytes = (int)(tokens * runs * xs);
+  S.xsum_bytes = kind == Q2_0 ? (int)((tokens * runs * 4 + 15) & ~15ll) : 0;
   const int64_t nmax = (15 + (int64_t)S.tile_rows * rb) / 16;  // whole chunks of an item, at most
   S.loads = (int)((nmax + SM_NT - 1) / SM_NT);
   return OK;
@@ -202,7 +230,7 @@ static int launch_stream(const StreamPlan& S0, const uint8_t* blocks, const uint
                          hipStream_t stream, bool dry) {
   StreamPlan S = S0;
   auto kern = k_stream_mv<KIND, XT, TM>;
-  const size_t dyn_lds = (size_t)S.x_bytes + SM_TILE;
+  const size_t dyn_lds = (size_t)S.x_bytes + S.xsum_bytes + SM_TILE;
   const size_t lds = dyn_lds + static_lds(kern);
   if (lds > LDS_BYTES) return fail(E_UNSUPPORTED, "stream matvec: %zu bytes of LDS", lds);
   if (dry) return OK;
