@@ -79,8 +79,8 @@ int sh_switch_matvec_generic(int kind, const void* blocks, const void* const* ex
  * out (n_mats, tokens, rows) in x's type. Q2_0 or IQ3_S with bf16 / fp16 activations, cols a multiple of 256 up
  * to 4096 (wider rows where the waves' column splits and the LDS ring allow: sh_stack_takes says), up to 16 tokens:
  * the MFMA kernels. Every other kind, and float32 activations: the exact-weight stream (float32 sums; the bits of
- * sh_switch_matvec_generic but for Q2_0, taken a run at a time as d (sum q x - sum x)), up to 8 tokens whose
- * activations fit 96 KiB of LDS, blocks and x 16-byte aligned.
+ * sh_switch_matvec_generic for the codebook kinds; Q2_0, IQ4_NL, IQ4_XS and Q3_K with their scales taken out of
+ * each run's sums), up to 8 tokens whose activations fit 96 KiB of LDS, blocks and x 16-byte aligned.
  * One streaming launch over all matrices (one per window of row tiles for the longest Q2_0 stacks).
  * workspace: sh_stack_workspace() bytes (none). */
 size_t sh_stack_workspace(int kind, int64_t n_mats, int64_t rows, int64_t cols, int64_t tokens, int x_dtype);

@@ -5,10 +5,11 @@
 //
 // Arithmetic: the generic kernels' own (blocks.hip k_window_matvec): P lanes share a row, lane `part` takes the
 // runs part, part + P, ... in order, each run's 32 weights decoded exactly (decode.h unpack32) and dotted with the
-// token's 32 activations in order, the P lanes' sums met by a butterfly: their bits, for every kind but Q2_0. A
-// Q2_0 run is taken as d (sum q x - sum x) (q the codes 0..3, sum x the run's activations summed once a matrix):
-// two VALU instructions a weight and a token (a conversion and an FMA) instead of four, different roundings (of
-// the same size). Where the bytes come from differs too:
+// token's 32 activations in order, the P lanes' sums met by a butterfly: their bits for the codebook kinds. The
+// kinds with a scale a run (or half run) take it, and the offset, out of the sums, with roundings of the same size:
+// Q2_0 d (sum q x - sum x) (q the codes 0..3 converted a byte at a time, sum x the run's activations summed once a
+// matrix): two VALU instructions a weight and a token instead of four; IQ4_NL / IQ4_XS dl sum kv[q] x; Q3_K
+// s (sum (q + 4h) x - 4 sum x) a half run. Where the bytes come from differs too:
 //   - persistent blocks of 256 threads each take a contiguous run of items (tile_rows rows of one matrix); an
 //     item's bytes, contiguous in the stack, are read with 16-byte loads (all 256 threads, consecutive chunks:
 //     fully coalesced) into registers while the item before is multiplied, then written to LDS;
@@ -65,6 +66,26 @@ template <typename XT> __device__ __forceinline__ float dot32_lds(const float* w
   return dot32<XT>(w, (const XT*)v);
 }
 
+// the same as two dots of 16 (the run's halves), each in order
+template <typename XT> __device__ __forceinline__ void dot32h_lds(const float* w, const uint8_t* xr, float& a0,
+                                                                  float& a1) {
+  constexpr int NV = 32 * (int)sizeof(XT) / 16;
+  u32x4 v[NV];
+#pragma unroll
+  for (int i = 0; i < NV; ++i) v[i] = *(const u32x4*)(xr + 16 * i);
+  const XT* x = (const XT*)v;
+  a0 = 0.0f, a1 = 0.0f;
+#pragma unroll
+  for (int j = 0; j < 16; ++j) {
+    a0 = fmaf(w[j], to_f32(x[j]), a0);
+    a1 = fmaf(w[16 + j], to_f32(x[16 + j]), a1);
+  }
+}
+
+// activations a sum of the staging covers, for the kinds whose runs subtract an offset times them: Q2_0 a run,
+// Q3_K half a run (one scale each); 0: none
+template <int KIND> constexpr int stream_sum_group() { return KIND == Q2_0 ? 32 : KIND == Q3_K ? 16 : 0; }
+
 template <int KIND, typename XT, int TM>
 __global__ __launch_bounds__(SM_NT) void k_stream_mv(const uint8_t* __restrict__ blocks, StreamPlan S,
                                                      const XT* __restrict__ x, XT* __restrict__ out,
@@ -73,7 +94,7 @@ __global__ __launch_bounds__(SM_NT) void k_stream_mv(const uint8_t* __restrict__
   extern __shared__ u32x4 dyn[];
   uint8_t* tab = (uint8_t*)tab4;
   uint8_t* xl = (uint8_t*)dyn;              // the current matrix's activations: [token][run], x_stride bytes a run
-  float* xsum = (float*)((uint8_t*)dyn + S.x_bytes);  // Q2_0: each run's sum of activations [token][run]
+  float* xsum = (float*)((uint8_t*)dyn + S.x_bytes);  // sums of activations [token][run][32 / SUMG]
   uint8_t* tl = (uint8_t*)dyn + S.x_bytes + S.xsum_bytes;  // the item's bytes from the 16-byte chunk holding its first
   const int tid = threadIdx.x;
   const int64_t first = (int64_t)blockIdx.x * S.per, last = min(S.items, first + S.per);
@@ -121,7 +142,7 @@ __global__ __launch_bounds__(SM_NT) void k_stream_mv(const uint8_t* __restrict__
   };
   // matrix m's activations into LDS: x[m] is [tokens][cols], so 16-byte vector v lies in run (t * runs + n)
   auto stage_x = [&](int64_t m) {
-    constexpr int RB = 32 * (int)sizeof(XT);
+    constexpr int RB = 32 * (int)sizeof(XT), SUMG = stream_sum_group<KIND>();
     const uint8_t* xs = (const uint8_t*)(x + m * S.tokens * S.cols);
     const int nv = S.tokens * S.cols * (int)sizeof(XT) / 16;
     for (int v0 = 0; v0 < nv; v0 += SM_NT) {  // every lane the same rounds (the sums' lane exchanges)
@@ -133,17 +154,17 @@ __global__ __launch_bounds__(SM_NT) void k_stream_mv(const uint8_t* __restrict__
         xv = *(const u32x4*)(xs + 16 * v);
         *(u32x4*)(xl + tr * S.x_stride + o) = xv;
       }
-      if constexpr (KIND == Q2_0) {
-        // the run's sum: each lane its vector's elements in order, then the RB / 16 lanes of the run (consecutive,
-        // an aligned group: nv is whole runs) by a butterfly
-        constexpr int NE = 16 / (int)sizeof(XT), NL = RB / 16;
+      if constexpr (SUMG > 0) {
+        // the sums of SUMG activations (a run, or half one): each lane its vector's elements in order, then the
+        // group's NL lanes (consecutive, an aligned group: nv is whole runs) by a butterfly
+        constexpr int NE = 16 / (int)sizeof(XT), NL = SUMG / NE;
         const XT* e = (const XT*)&xv;
         float p = 0.0f;
 #pragma unroll
         for (int i = 0; i < NE; ++i) p += to_f32(e[i]);
 #pragma unroll
         for (int o2 = NL / 2; o2 > 0; o2 >>= 1) p += __shfl_xor(p, o2);
-        if (in && o == 0) xsum[tr] = p;
+        if (in && v % NL == 0) xsum[v / NL] = p;
       }
     }
   };
@@ -177,6 +198,51 @@ __global__ __launch_bounds__(SM_NT) void k_stream_mv(const uint8_t* __restrict__
           for (int t = 0; t < TM; ++t)
             if (t < S.tokens)
               sum[t] += d * (dot32_lds<XT>(w, xl + (t * S.runs + n) * S.x_stride) - xsum[t * S.runs + n]);
+        } else if constexpr (KIND == IQ4_NL || KIND == IQ4_XS) {  // the scale once a run: dl sum kv[q] x
+          const uint8_t* q;
+          float dl;
+          if constexpr (KIND == IQ4_NL) {
+            q = row + n * 18 + 2;
+            dl = half_at(q - 2);
+          } else {
+            const uint8_t* b = row + (n >> 3) * 136;
+            const int ib = n & 7;
+            const uint32_t ls = (((uint32_t)b[4 + ib / 2] >> (4 * (ib & 1))) & 15u) | (((rd16(b + 2) >> (2 * ib)) & 3u) << 4);
+            dl = half_at(b) * ((float)ls - 32.0f);
+            q = b + 8 + 16 * ib;
+          }
+          const int8_t* kv = (const int8_t*)tab;
+#pragma unroll
+          for (int i = 0; i < 16; ++i) {
+            const uint32_t c = q[i];
+            w[i] = (float)kv[c & 15];
+            w[16 + i] = (float)kv[c >> 4];
+          }
+#pragma unroll
+          for (int t = 0; t < TM; ++t)
+            if (t < S.tokens) sum[t] += dl * dot32_lds<XT>(w, xl + (t * S.runs + n) * S.x_stride);
+        } else if constexpr (KIND == Q3_K) {  // two scales of 16: s (sum (q + 4h) x - 4 sum x) each
+          const uint8_t* b = row + (n >> 3) * 110;
+          const int r = n & 7, shift = 2 * (r & 3);
+          const uint8_t* q = b + 32 + 32 * (r >> 2);
+          const float d = half_at(b + 108);
+          const float s0 = d * q3k_scale(b + 96, 2 * r), s1 = d * q3k_scale(b + 96, 2 * r + 1);
+#pragma unroll
+          for (int k = 0; k < 8; ++k) {  // weights 4k .. 4k + 3: (q >> shift & 3) | (h >> r & 1) << 2, 0..7
+            uint32_t m = ((rd32(q + 4 * k) >> shift) & 0x03030303u) | (((rd32(b + 4 * k) >> r) & 0x01010101u) << 2);
+            asm("" : "+v"(m));
+#pragma unroll
+            for (int i = 0; i < 4; ++i) w[4 * k + i] = (float)((m >> (8 * i)) & 0xffu);
+          }
+#pragma unroll
+          for (int t = 0; t < TM; ++t) {
+            if (t < S.tokens) {
+              float a0, a1;
+              dot32h_lds<XT>(w, xl + (t * S.runs + n) * S.x_stride, a0, a1);
+              const float* xs2 = xsum + 2 * (t * S.runs + n);
+              sum[t] += s0 * (a0 - 4.0f * xs2[0]) + s1 * (a1 - 4.0f * xs2[1]);
+            }
+          }
         } else {
           unpack32<KIND>(row, n, w, tab);
 #pragma unroll
@@ -219,7 +285,8 @@ static int stream_plan(int kind, int x_dtype, const void* blocks, const void* x,
   S.items_per_mat = (int)((rows + S.tile_rows - 1) / S.tile_rows);
   S.items = n_mats * S.items_per_mat;
   S.x_stride = (int)xs, S.x_bytes = (int)(tokens * runs * xs);
-  S.xsum_bytes = kind == Q2_0 ? (int)((tokens * runs * 4 + 15) & ~15ll) : 0;
+  const int sums = kind == Q2_0 ? 1 : kind == Q3_K ? 2 : 0;  // a run's (stream_sum_group)
+  S.xsum_bytes = (int)((tokens * runs * sums * 4 + 15) & ~15ll);
   const int64_t nmax = (15 + (int64_t)S.tile_rows * rb) / 16;  // whole chunks of an item, at most
   S.loads = (int)((nmax + SM_NT - 1) / SM_NT);
   return OK;

@@ -1,7 +1,8 @@
 """The streaming matvec of exact weights (every kind, float32 / bf16 / fp16 activations, one layer or a stack of
-matrices): the oracle's products within the path's tolerances; for every kind but Q2_0 (whose runs it takes as
-d (sum q x - sum x)) the generic expert kernel's bits exactly (the same runs a lane, the same order of sums); a
-token's bits whatever its window, and a layer's the same alone or in a stack."""
+matrices): the oracle's products within the path's tolerances; for the kinds whose runs it takes as the generic
+kernels do (not Q2_0, IQ4_NL, IQ4_XS, Q3_K, whose scales and offsets it takes out of the sums) the generic expert
+kernel's bits exactly (the same runs a lane, the same order of sums); a token's bits whatever its window, and a
+layer's the same alone or in a stack."""
 
 import numpy as np
 import pytest
@@ -30,10 +31,13 @@ def act(rng, shape, dtype):
     return t, t.float().numpy()
 
 
+FACTORED = ("Q2_0", "IQ4_NL", "IQ4_XS", "Q3_K")  # kinds whose runs the stream takes with the scales outside
+
+
 def streamed(kind, dtype):
     """Whether window_matvec takes the exact-weight stream (not the MFMA kernels) for this kind and dtype, with the
-    generic kernel's bits (every kind but Q2_0)."""
-    return kind != "Q2_0" and not (kind == "IQ3_S" and dtype != "float32")
+    generic kernel's bits (its runs' arithmetic)."""
+    return kind not in FACTORED and not (kind == "IQ3_S" and dtype != "float32")
 
 
 def generic(b, kind, shape, x, dev):
@@ -95,28 +99,30 @@ def test_rows_not_whole_chunks(kind, cols, tokens, tables, dev):
     got = SB.stack_matvec(b, kind, (n, R, cols), x.to(dev)).cpu()
     want = np.einsum("mrc,mtc->mtr", w.astype(np.float64), xv.astype(np.float64))
     assert rel_err(got.numpy(), want) <= TOL["float32"]
-    if kind != "Q2_0":
+    if kind not in FACTORED:
         assert torch.equal(got, generic(b, kind, (n, R, cols), x.to(dev), dev).cpu())
     one = SB.window_matvec(b[: R * SB.row_bytes(kind, cols)], kind, R, cols, x[0].to(dev)).cpu()
     assert torch.equal(one, got[0])
 
 
 @pytest.mark.parametrize("dtype", ["float32", "bfloat16"])
-def test_negative_scales(dtype, tables, dev):
-    """Q2_0 blocks with negative scales (the stream takes d out of each run's sum): rows of both signs against the
-    oracle, a layer alone the bits of the same layer in the stack."""
-    n, R, C = 2, 64, 576  # 9 blocks a row: the MFMA kernels do not take it in bf16 either
-    raw, _ = mats("Q2_0", n, R, C, 370, tables)
-    blk = raw.reshape(-1, 18)
-    blk[::2, 1] |= 0x80  # every other block's fp16 scale negative
-    w = OB.dequantize(raw, "Q2_0", (n, R, C), tables)
+@pytest.mark.parametrize("kind, cols, block, d_at", [("Q2_0", 576, 18, 0), ("IQ4_NL", 576, 18, 0),
+                                                     ("IQ4_XS", 768, 136, 0), ("Q3_K", 768, 110, 108)])
+def test_negative_scales(kind, cols, block, d_at, dtype, tables, dev):
+    """Blocks with negative scales (the stream takes the scales out of each run's sums): rows of both signs against
+    the oracle, a layer alone the bits of the same layer in the stack."""
+    n, R, C = 2, 64, cols  # Q2_0 at 9 blocks a row: the MFMA kernels do not take it in bf16 either
+    raw, _ = mats(kind, n, R, C, 370, tables)
+    blk = raw.reshape(-1, block)
+    blk[::2, d_at + 1] |= 0x80  # every other block's fp16 scale negative
+    w = OB.dequantize(raw, kind, (n, R, C), tables)
     rng = np.random.default_rng(371)
     x, xv = act(rng, (n, 3, C), dtype)
     b = torch.from_numpy(raw).to(dev)
-    got = SB.stack_matvec(b, "Q2_0", (n, R, C), x.to(dev)).cpu()
+    got = SB.stack_matvec(b, kind, (n, R, C), x.to(dev)).cpu()
     want = np.einsum("mrc,mtc->mtr", w.astype(np.float64), xv.astype(np.float64))
     assert rel_err(got.float().numpy(), want) <= TOL[dtype]
-    one = SB.window_matvec(b[R * SB.row_bytes("Q2_0", C):], "Q2_0", R, C, x[1].to(dev)).cpu()
+    one = SB.window_matvec(b[R * SB.row_bytes(kind, C):], kind, R, C, x[1].to(dev)).cpu()
     assert torch.equal(one, got[1])
 
 
