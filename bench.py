@@ -166,12 +166,13 @@ COUNTER_PASSES = {  # six a pass: derived counters can take more than one of the
     "lds": ["SQ_LDS_BANK_CONFLICT", "SQ_LDS_IDX_ACTIVE", "SQ_VALU_MFMA_BUSY_CYCLES", "SQ_WAIT_ANY",
             "SQ_ACTIVE_INST_LDS", "SQ_CYCLES"],
 }
-COUNTER_KERNELS = {"prefill": "k_tile_stream", "stack_iq3s": "k_stack_mv"}
+COUNTER_KERNELS = {"prefill": "k_tile_stream", "stack_iq3s": "k_stack_mv", "stream_q2_f32": "k_stream_mv"}
 
 
 def counters_run(workload):
-    """The workload an instruction-mix counter run reads: the C5 prefill layer's two stream passes (prefill) or
-    the C2 IQ3_S stream at one token (stack_iq3s), a few launches each."""
+    """The workload an instruction-mix counter run reads: the C5 prefill layer's two stream passes (prefill), the
+    C2 IQ3_S stream at one token (stack_iq3s) or the C1 stream, Q2_0 with float32 vectors (stream_q2_f32), a few
+    launches each."""
     import numpy as np
     import torch
 
@@ -194,13 +195,14 @@ def counters_run(workload):
         idx = SF.top_k(logits, K)
         for _ in range(3):
             SB._tiled_glu(x[None], idx[None], up, gate, down)
-    elif workload == "stack_iq3s":
+    elif workload in ("stack_iq3s", "stream_q2_f32"):
+        kind, dt = ("IQ3_S", torch.bfloat16) if workload == "stack_iq3s" else ("Q2_0", torch.float32)
         R, C = 3072, 2048
-        n = -(-600_000_000 // (R * SB.row_bytes("IQ3_S", C)))
-        blocks = synth.random_blocks_gpu("IQ3_S", n * R, C, 7, dev)
-        x = torch.randn(n, 1, C, device=dev).to(torch.bfloat16)
+        n = -(-600_000_000 // (R * SB.row_bytes(kind, C)))
+        blocks = synth.random_blocks_gpu(kind, n * R, C, 7, dev)
+        x = torch.randn(n, 1, C, device=dev).to(dt)
         for _ in range(3):
-            SB.stack_matvec(blocks, "IQ3_S", (n, R, C), x)
+            SB.stack_matvec(blocks, kind, (n, R, C), x)
     else:
         raise SystemExit(f"--counters-run: {workload} (one of {sorted(COUNTER_KERNELS)})")
     torch.cuda.synchronize()
@@ -741,7 +743,7 @@ def main():
     ap.add_argument("--traffic-run", action="store_true", help="the counter runs' workload (under rocprofv3)")
     ap.add_argument("--traffic-summarize", metavar="DIR", help="the counter summary of two runs' output directory")
     ap.add_argument("--counters-run", metavar="WORKLOAD", help="an instruction-mix counter run's workload "
-                    "(prefill, stack_iq3s; under rocprofv3)")
+                    "(prefill, stack_iq3s, stream_q2_f32; under rocprofv3)")
     ap.add_argument("--counters-summarize", nargs=2, metavar=("DIR", "WORKLOAD"),
                     help="the instruction-mix summary of the two passes' output directory")
     args = ap.parse_args()
