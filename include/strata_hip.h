@@ -63,14 +63,16 @@ int sh_dequantize(int kind, const void* blocks, const void* tables, int64_t n_ma
 
 /* strata_mlx/blocks.py:407-436 (BlockSwitchLinear.__call__, kernel _MATVEC 196-220):
  * out[pair, r] = W[idx[pair], r, :] . x[pair / share, :], out in x's dtype. bf16/fp16 activations of Q2_0 and
- * IQ3_S take the MFMA path, everything else exact float32 weights and sums. Pairs sharing an expert read its
- * blocks once. `workspace` may be NULL when sh_switch_workspace() is 0. */
+ * IQ3_S take the MFMA path, everything else exact float32 weights and sums (the exact-weight stream over the
+ * pairs where it takes them: blocks and x 16-byte aligned). Pairs sharing an expert read its blocks once (MFMA
+ * path). `workspace` may be NULL when sh_switch_workspace() is 0. */
 size_t sh_switch_workspace(int kind, int64_t rows, int64_t cols, int64_t pairs, int x_dtype);
 int sh_switch_matvec(int kind, const void* blocks, const void* tables, int64_t experts, int64_t rows, int64_t cols,
                      const int32_t* idx, int64_t pairs, const void* x, int x_dtype, int64_t share, void* out,
                      void* workspace, size_t workspace_bytes, void* stream);
 /* the same product with exact float32 weights and sums for every kind and dtype (no MFMA); `expert_ptrs`
- * (device array of per-pair block pointers) replaces blocks + idx when not NULL. */
+ * (device array of per-pair block pointers) replaces blocks + idx when not NULL (then a block a few rows a pair;
+ * with blocks + idx the exact-weight stream where it takes the pairs). */
 int sh_switch_matvec_generic(int kind, const void* blocks, const void* const* expert_ptrs, const void* tables,
                              int64_t experts, int64_t rows, int64_t cols, const int32_t* idx, int64_t pairs,
                              const void* x, int x_dtype, int64_t share, void* out, void* stream);

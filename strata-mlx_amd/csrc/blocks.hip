@@ -279,6 +279,11 @@ int sh_switch_matvec_generic(int kind, const void* blocks, const void* const* ex
   if (share <= 0) return fail(E_ARG, "switch_matvec: share %lld", (long long)share);
   if ((!blocks && !expert_ptrs) || (!expert_ptrs && !idx) || !x || !out || (needs_tables(kind) && !tables))
     return fail(E_ARG, "switch_matvec: null pointer");
+  if (!expert_ptrs) {  // the exact-weight stream over the pairs where it takes them, else a block a few rows a pair
+    st = stream_matvec(false, kind, blocks, tables, pairs, rows, cols, x, x_dtype, 1, out, stream, idx, n_experts,
+                       share);
+    if (st != E_UNSUPPORTED) return st;
+  }
   int P = lanes_per_row(cols / 32);
   return with_kind(kind, [&](auto kc) {
     constexpr int K = decltype(kc)::value;
@@ -308,7 +313,7 @@ int sh_window_matvec(int kind, const void* blocks, const void* tables, int64_t r
   if (tokens <= 0) return OK;
   if (tokens > 8) return fail(E_SHAPE, "window_matvec: %lld tokens (a window is at most 8)", (long long)tokens);
   if (!blocks || !x || !out || (needs_tables(kind) && !tables)) return fail(E_ARG, "window_matvec: null pointer");
-  // the streaming kernel where it takes the layer (the same bits), else a block a few rows
+  // the exact-weight stream where it takes the layer, else a block a few rows
   st = stream_matvec(false, kind, blocks, tables, 1, rows, cols, x, x_dtype, tokens, out, stream);
   if (st != E_UNSUPPORTED) return st;
   int P = lanes_per_row(cols / 32);

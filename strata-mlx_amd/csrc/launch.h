@@ -100,8 +100,10 @@ inline void row_layout(int64_t rbytes, bool aligned, int& rstride, int& padded) 
 }
 
 // the streaming matvec of every kind (stream.hip): out[m][t] = W_m . x[m][t] for n_mats matrices and 1-8 tokens,
-// the generic kernels' arithmetic; E_UNSUPPORTED where it does not take the arguments (dry: checks and plan only)
+// or (idx) out[m] = W[idx[m]] . x[m / share] for n_mats pairs over a stack of n_experts; exact weights and float32
+// sums; E_UNSUPPORTED where it does not take the arguments (dry: checks and plan only)
 int stream_matvec(bool dry, int kind, const void* blocks, const void* tables, int64_t n_mats, int64_t rows,
-                  int64_t cols, const void* x, int x_dtype, int64_t tokens, void* out, void* stream);
+                  int64_t cols, const void* x, int x_dtype, int64_t tokens, void* out, void* stream,
+                  const int32_t* idx = nullptr, int64_t n_experts = 0, int64_t share = 1);
 
 }  // namespace sh

@@ -86,10 +86,13 @@ template <typename XT> __device__ __forceinline__ void dot32h_lds(const float* w
 // Q3_K half a run (one scale each); 0: none
 template <int KIND> constexpr int stream_sum_group() { return KIND == Q2_0 ? 32 : KIND == Q3_K ? 16 : 0; }
 
+// idx: NULL (matrix m is the stack's m-th, its activations x[m]) or the expert of each pair m (a pair naming no
+// expert, outside [0, n_experts), gets zeros), its activations x[m / share] (one token a pair)
 template <int KIND, typename XT, int TM>
 __global__ __launch_bounds__(SM_NT) void k_stream_mv(const uint8_t* __restrict__ blocks, StreamPlan S,
                                                      const XT* __restrict__ x, XT* __restrict__ out,
-                                                     const uint8_t* __restrict__ tabs) {
+                                                     const uint8_t* __restrict__ tabs, const int32_t* __restrict__ idx,
+                                                     int n_experts, int share) {
   __shared__ u32x4 tab4[lds_tab_bytes(KIND) / 16];
   extern __shared__ u32x4 dyn[];
   uint8_t* tab = (uint8_t*)tab4;
@@ -107,6 +110,7 @@ __global__ __launch_bounds__(SM_NT) void k_stream_mv(const uint8_t* __restrict__
   struct Span {
     int64_t m;
     int r0, nr, lead, nfull, ntail;
+    bool valid;  // the matrix exists (a pair's expert in range): else no loads, zeros out
     const uint8_t* a16;
   };
   auto span = [&](int64_t item) {
@@ -114,10 +118,17 @@ __global__ __launch_bounds__(SM_NT) void k_stream_mv(const uint8_t* __restrict__
     s.m = item / S.items_per_mat;
     s.r0 = (int)(item - s.m * S.items_per_mat) * S.tile_rows;
     s.nr = min(S.tile_rows, S.rows - s.r0);
-    const int64_t off = s.m * S.mat_bytes + (int64_t)s.r0 * S.rbytes;
+    int64_t mat = s.m;
+    s.valid = true;
+    if (idx) {
+      const int e = idx[s.m];
+      s.valid = e >= 0 && e < n_experts;
+      mat = s.valid ? e : 0;
+    }
+    const int64_t off = mat * S.mat_bytes + (int64_t)s.r0 * S.rbytes;
     s.a16 = blocks + (off & ~(int64_t)15);  // from the kernel argument: global loads
     s.lead = (int)(off & 15);
-    const int n = s.lead + s.nr * (int)S.rbytes;
+    const int n = s.valid ? s.lead + s.nr * (int)S.rbytes : 0;
     s.nfull = n >> 4;
     s.ntail = n & 15;
     return s;
@@ -143,7 +154,7 @@ __global__ __launch_bounds__(SM_NT) void k_stream_mv(const uint8_t* __restrict__
   // matrix m's activations into LDS: x[m] is [tokens][cols], so 16-byte vector v lies in run (t * runs + n)
   auto stage_x = [&](int64_t m) {
     constexpr int RB = 32 * (int)sizeof(XT), SUMG = stream_sum_group<KIND>();
-    const uint8_t* xs = (const uint8_t*)(x + m * S.tokens * S.cols);
+    const uint8_t* xs = (const uint8_t*)(x + m / share * S.tokens * S.cols);
     const int nv = S.tokens * S.cols * (int)sizeof(XT) / 16;
     for (int v0 = 0; v0 < nv; v0 += SM_NT) {  // every lane the same rounds (the sums' lane exchanges)
       const int v = v0 + tid;
@@ -184,7 +195,7 @@ __global__ __launch_bounds__(SM_NT) void k_stream_mv(const uint8_t* __restrict__
     __syncthreads();
     for (int r0 = 0; r0 < s.nr; r0 += S.rp) {  // passes: every lane the same (the sums' lane exchanges)
       const int r = r0 + rin;
-      const bool act = r < s.nr;  // the P lanes of a row alike
+      const bool act = r < s.nr && s.valid;  // the P lanes of a row alike
       const uint8_t* row = tl + s.lead + (int64_t)r * S.rbytes;
       float w[32], sum[TM];
 #pragma unroll
@@ -254,7 +265,7 @@ __global__ __launch_bounds__(SM_NT) void k_stream_mv(const uint8_t* __restrict__
       for (int t = 0; t < TM; ++t) {
         if (t < S.tokens) {
           const float total = lanes_sum(sum[t], S.P);
-          if (act && part == 0) out[(s.m * S.tokens + t) * S.rows + s.r0 + r] = from_f32<XT>(total);
+          if (r < s.nr && part == 0) out[(s.m * S.tokens + t) * S.rows + s.r0 + r] = from_f32<XT>(total);
         }
       }
     }
@@ -294,7 +305,7 @@ static int stream_plan(int kind, int x_dtype, const void* blocks, const void* x,
 
 template <int KIND, typename XT, int TM>
 static int launch_stream(const StreamPlan& S0, const uint8_t* blocks, const uint8_t* tabs, const XT* x, XT* out,
-                         hipStream_t stream, bool dry) {
+                         hipStream_t stream, bool dry, const int32_t* idx, int n_experts, int share) {
   StreamPlan S = S0;
   auto kern = k_stream_mv<KIND, XT, TM>;
   const size_t dyn_lds = (size_t)S.x_bytes + S.xsum_bytes + SM_TILE;
@@ -305,18 +316,24 @@ static int launch_stream(const StreamPlan& S0, const uint8_t* blocks, const uint
   const int64_t cap = (int64_t)device_cus() * bpc;
   S.per = (S.items + cap - 1) / cap;
   const int64_t grid = (S.items + S.per - 1) / S.per;
-  hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(SM_NT), dyn_lds, stream, blocks, S, x, out, tabs);
+  hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(SM_NT), dyn_lds, stream, blocks, S, x, out, tabs, idx,
+                     n_experts, share);
   return check_launch("stream matvec");
 }
 
 // the streaming matvec's checks, plan and launch (dry: checks and plan only); E_UNSUPPORTED where it does not take
-// the arguments
+// the arguments. With idx, the n_mats "matrices" are pairs: pair m multiplies expert idx[m] of the stack's
+// n_experts by x[m / share] (one token a pair).
 int stream_matvec(bool dry, int kind, const void* blocks, const void* tables, int64_t n_mats, int64_t rows,
-                  int64_t cols, const void* x, int x_dtype, int64_t tokens, void* out, void* stream) {
+                  int64_t cols, const void* x, int x_dtype, int64_t tokens, void* out, void* stream,
+                  const int32_t* idx, int64_t n_experts, int64_t share) {
   int st = check_rows(kind, rows, cols, "stream matvec");
   if (st) return st;
   if (!blocks || !x || (!out && !dry) || (needs_tables(kind) && !tables))
     return fail(E_ARG, "stream matvec: null pointer");
+  if (idx && (tokens != 1 || share < 1 || n_experts < 0 || n_experts > (1ll << 31) - 1))
+    return fail(E_UNSUPPORTED, "stream matvec: pairs of %lld tokens, share %lld", (long long)tokens,
+                (long long)share);
   StreamPlan S;
   st = stream_plan(kind, x_dtype, blocks, x, n_mats, rows, cols, tokens, S);
   if (st) return st;
@@ -326,9 +343,9 @@ int stream_matvec(bool dry, int kind, const void* blocks, const void* tables, in
       using XT = std::remove_pointer_t<decltype(tp)>;
       if (tokens == 1)
         return launch_stream<K, XT, 1>(S, (const uint8_t*)blocks, (const uint8_t*)tables, (const XT*)x, (XT*)out,
-                                       (hipStream_t)stream, dry);
+                                       (hipStream_t)stream, dry, idx, (int)n_experts, (int)share);
       return launch_stream<K, XT, 8>(S, (const uint8_t*)blocks, (const uint8_t*)tables, (const XT*)x, (XT*)out,
-                                     (hipStream_t)stream, dry);
+                                     (hipStream_t)stream, dry, idx, (int)n_experts, (int)share);
     });
   });
 }

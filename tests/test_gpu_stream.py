@@ -41,11 +41,13 @@ def streamed(kind, dtype):
 
 
 def generic(b, kind, shape, x, dev):
-    """The generic expert kernel, pair t = matrix m's token t: the reference bits of the stream."""
+    """The generic expert kernel (matvec_separate: a buffer a pair), pair t = matrix m's token t: the reference
+    bits of the stream."""
     n, rows, cols = shape
     tokens = x.shape[-2]
-    idx = torch.arange(n, dtype=torch.int32).repeat_interleave(tokens)
-    return SB.switch_matvec(b, kind, shape, idx.to(dev), x.reshape(-1, cols), 1).reshape(n, tokens, rows)
+    mat = rows * SB.row_bytes(kind, cols)
+    experts = [b[m * mat : (m + 1) * mat] for m in range(n) for _ in range(tokens)]
+    return SB.matvec_separate(experts, kind, rows, cols, x.reshape(-1, cols), 1).reshape(n, tokens, rows)
 
 
 @pytest.mark.parametrize("kind", KINDS)
@@ -167,3 +169,33 @@ def test_the_stream_refuses_what_it_does_not_take(tables, dev):
     # one layer of them still multiplies, through the generic window kernel
     got = SB.window_matvec(wide, "IQ4_NL", 4, 4096, torch.ones((8, 4096)).to(dev))
     assert got.shape == (8, 4)
+
+
+@pytest.mark.parametrize("kind", KINDS)
+@pytest.mark.parametrize("dtype", ["float32", "bfloat16"])
+@pytest.mark.parametrize("share", [1, 3])
+def test_expert_pairs_through_the_stream(kind, dtype, share, tables, dev):
+    """switch_matvec's pairs (each its expert of the stack and its row of x, pairs sharing a row, a pair naming no
+    expert): the oracle's products, zeros for the pair without an expert, the generic kernel's bits for the kinds
+    whose runs the stream takes as it does."""
+    E, R, C = 5, 96, 512
+    raw, w = mats(kind, E, R, C, 380, tables)
+    idx = np.array([4, 0, 2, 2, 7, 1, 0, 3, -1], dtype=np.int32)  # 7 and -1 name no expert
+    rng = np.random.default_rng(381)
+    x, xv = act(rng, (-(-len(idx) // share), C), dtype)
+    b = torch.from_numpy(raw).to(dev)
+    if kind in ("Q2_0", "IQ3_S") and dtype != "float32":
+        pytest.skip("the MFMA kernels take these pairs")
+    got = SB.switch_matvec(b, kind, (E, R, C), torch.from_numpy(idx).to(dev), x.to(dev), share).cpu()
+    for p, e in enumerate(idx):
+        if 0 <= e < E:
+            want = w[e].astype(np.float64) @ xv[p // share].astype(np.float64)
+            assert rel_err(got[p].float().numpy(), want) <= TOL[dtype]
+        else:
+            assert not got[p].any()
+    if kind not in FACTORED:
+        mat = R * SB.row_bytes(kind, C)
+        ok = [p for p, e in enumerate(idx) if 0 <= e < E]
+        sep = SB.matvec_separate([b[idx[p] * mat : (idx[p] + 1) * mat] for p in ok], kind, R, C,
+                                 torch.stack([x[p // share] for p in ok]).to(dev), 1).cpu()
+        assert torch.equal(got[ok], sep)
