@@ -199,3 +199,31 @@ def test_expert_pairs_through_the_stream(kind, dtype, share, tables, dev):
         sep = SB.matvec_separate([b[idx[p] * mat : (idx[p] + 1) * mat] for p in ok], kind, R, C,
                                  torch.stack([x[p // share] for p in ok]).to(dev), 1).cpu()
         assert torch.equal(got[ok], sep)
+
+
+@pytest.mark.parametrize("kind", ["Q2_0", "IQ2_S"])
+def test_activations_off_16_bytes_take_the_generic_kernel(kind, tables, dev):
+    """Activations that do not start on 16 bytes (a view one element in) are not the stream's: the window and the
+    pairs go to the generic kernel, the stack is refused; the products are the same within the tolerance (the
+    same bits for a codebook kind)."""
+    E, R, C = 3, 64, 512
+    raw, w = mats(kind, E, R, C, 390, tables)
+    b = torch.from_numpy(raw).to(dev)
+    rng = np.random.default_rng(391)
+    xs, xv = act(rng, (1, 2 * C + 1), "float32")
+    off = xs.to(dev)[0, 1 : 1 + 2 * C].reshape(2, C)  # 4 bytes past a 16-byte boundary
+    ok = off.clone()
+    assert off.data_ptr() % 16 and ok.data_ptr() % 16 == 0
+    mat = R * SB.row_bytes(kind, C)
+    got = SB.window_matvec(b[:mat], kind, R, C, off).cpu()
+    ref = SB.window_matvec(b[:mat], kind, R, C, ok).cpu()
+    want = xv[0, 1 : 1 + 2 * C].reshape(2, C).astype(np.float64) @ w[0].T.astype(np.float64)
+    assert rel_err(got.numpy(), want) <= 1e-5 and rel_err(ref.numpy(), want) <= 1e-5
+    idx = torch.tensor([2, 0], dtype=torch.int32).to(dev)
+    pairs = SB.switch_matvec(b, kind, (E, R, C), idx, off, 1).cpu()
+    assert rel_err(pairs[0].numpy(), w[2].astype(np.float64) @ xv[0, 1 : 1 + C].astype(np.float64)) <= 1e-5
+    if kind not in FACTORED:
+        assert torch.equal(got, ref)
+        assert torch.equal(pairs, SB.switch_matvec(b, kind, (E, R, C), idx, ok, 1).cpu())
+    with pytest.raises(Exception, match="aligned"):
+        SB.stack_matvec(b[:mat], kind, (1, R, C), off[None])
