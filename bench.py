@@ -667,9 +667,11 @@ def moe_pass(layers, batches, args, dev, iq3s=False):
                 gu_graph.replay()
             torch.cuda.synchronize()
             ev = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
+            marks = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]  # each pass's end
             ev[0].record(stream)
-            for _ in range(args.steps):
+            for i in range(args.steps):
                 graph.replay()
+                marks[i].record(stream)
             ev[1].record(stream)
             ev[2].record(stream)
             for _ in range(args.steps):
@@ -708,7 +710,10 @@ def moe_pass(layers, batches, args, dev, iq3s=False):
         ms = ev[0].elapsed_time(ev[1])
         gu_ms = ev[2].elapsed_time(ev[3])
         n_layers = args.steps * len(layers)
+        passes = np.array([(ev[0] if i == 0 else marks[i - 1]).elapsed_time(marks[i]) for i in range(args.steps)])
         per_batch[b] = {"us_per_layer": round(ms * 1e3 / n_layers, 3),
+                        "us_per_layer_median": round(float(np.median(passes)) * 1e3 / len(layers), 3),
+                        "us_per_layer_p10": round(float(np.percentile(passes, 10)) * 1e3 / len(layers), 3),
                         "GBps": round(bytes_pass * args.steps / (ms * 1e-3) / 1e9, 1),
                         "unique_experts_mean": round(float(np.mean(uniq)), 2),
                         "tok_per_s": round(b * args.steps / (ms * 1e-3), 1),
