@@ -57,7 +57,8 @@ int sh_kind_block(int kind, int* weights_per_block, int* bytes_per_block);
 size_t sh_tables_bytes(void);
 
 /* strata_mlx/blocks.py:397-404 (dequantize) and 261-270 (_DEQUANT): every weight of n_mats (rows x cols)
- * matrices, out_dtype F32 (exact), F16 or BF16 (one rounding). */
+ * matrices, out_dtype F32 (exact), F16 or BF16 (one rounding). Coalesced 16-byte loads and stores where the blocks
+ * and the output are 16-byte aligned and an output row fits 32 KiB, else a run a thread: the same values. */
 int sh_dequantize(int kind, const void* blocks, const void* tables, int64_t n_mats, int64_t rows, int64_t cols,
                   void* out, int out_dtype, void* stream);
 
@@ -71,8 +72,9 @@ int sh_switch_matvec(int kind, const void* blocks, const void* tables, int64_t e
                      const int32_t* idx, int64_t pairs, const void* x, int x_dtype, int64_t share, void* out,
                      void* workspace, size_t workspace_bytes, void* stream);
 /* the same product with exact float32 weights and sums for every kind and dtype (no MFMA); `expert_ptrs`
- * (device array of per-pair block pointers) replaces blocks + idx when not NULL (then a block a few rows a pair;
- * with blocks + idx the exact-weight stream where it takes the pairs). */
+ * (device array of per-pair block pointers, each inside an allocation that starts on 16 bytes) replaces blocks +
+ * idx when not NULL. The exact-weight stream where it takes the pairs (x 16-byte aligned), else a block a few rows
+ * a pair. */
 int sh_switch_matvec_generic(int kind, const void* blocks, const void* const* expert_ptrs, const void* tables,
                              int64_t experts, int64_t rows, int64_t cols, const int32_t* idx, int64_t pairs,
                              const void* x, int x_dtype, int64_t share, void* out, void* stream);

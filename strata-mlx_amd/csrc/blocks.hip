@@ -256,6 +256,10 @@ int sh_dequantize(int kind, const void* blocks, const void* tables, int64_t n_ma
   if (st) return st;
   if (n_mats <= 0) return fail(E_SHAPE, "dequantize: %lld matrices", (long long)n_mats);
   if (!blocks || !out || (needs_tables(kind) && !tables)) return fail(E_ARG, "dequantize: null pointer");
+  if (out_dtype != F32 && out_dtype != F16 && out_dtype != BF16) return fail(E_DTYPE, "unknown dtype %d", out_dtype);
+  // coalesced loads and stores where the stream takes the tensor, else a run a thread
+  st = dequant_stream(kind, blocks, tables, n_mats * rows, cols, out, out_dtype, stream);
+  if (st != E_UNSUPPORTED) return st;
   int64_t total = n_mats * rows * (cols / 32);
   return with_kind(kind, [&](auto kc) {
     constexpr int K = decltype(kc)::value;
@@ -279,11 +283,10 @@ int sh_switch_matvec_generic(int kind, const void* blocks, const void* const* ex
   if (share <= 0) return fail(E_ARG, "switch_matvec: share %lld", (long long)share);
   if ((!blocks && !expert_ptrs) || (!expert_ptrs && !idx) || !x || !out || (needs_tables(kind) && !tables))
     return fail(E_ARG, "switch_matvec: null pointer");
-  if (!expert_ptrs) {  // the exact-weight stream over the pairs where it takes them, else a block a few rows a pair
-    st = stream_matvec(false, kind, blocks, tables, pairs, rows, cols, x, x_dtype, 1, out, stream, idx, n_experts,
-                       share);
-    if (st != E_UNSUPPORTED) return st;
-  }
+  // the exact-weight stream over the pairs where it takes them, else a block a few rows a pair
+  st = stream_matvec(false, kind, blocks, tables, pairs, rows, cols, x, x_dtype, 1, out, stream,
+                     expert_ptrs ? nullptr : idx, n_experts, share, expert_ptrs);
+  if (st != E_UNSUPPORTED) return st;
   int P = lanes_per_row(cols / 32);
   return with_kind(kind, [&](auto kc) {
     constexpr int K = decltype(kc)::value;

@@ -100,10 +100,16 @@ inline void row_layout(int64_t rbytes, bool aligned, int& rstride, int& padded) 
 }
 
 // the streaming matvec of every kind (stream.hip): out[m][t] = W_m . x[m][t] for n_mats matrices and 1-8 tokens,
-// or (idx) out[m] = W[idx[m]] . x[m / share] for n_mats pairs over a stack of n_experts; exact weights and float32
-// sums; E_UNSUPPORTED where it does not take the arguments (dry: checks and plan only)
+// or (idx) out[m] = W[idx[m]] . x[m / share] for n_mats pairs over a stack of n_experts, or (experts) the same with
+// pair m's blocks at experts[m]; exact weights and float32 sums; E_UNSUPPORTED where it does not take the arguments
+// (dry: checks and plan only)
 int stream_matvec(bool dry, int kind, const void* blocks, const void* tables, int64_t n_mats, int64_t rows,
                   int64_t cols, const void* x, int x_dtype, int64_t tokens, void* out, void* stream,
-                  const int32_t* idx = nullptr, int64_t n_experts = 0, int64_t share = 1);
+                  const int32_t* idx = nullptr, int64_t n_experts = 0, int64_t share = 1,
+                  const void* const* experts = nullptr);
+// dequantize (stream.hip) rows of `cols` weights to out_dtype by coalesced 16-byte loads and stores; E_UNSUPPORTED
+// where it does not take the tensor
+int dequant_stream(int kind, const void* blocks, const void* tables, int64_t rows, int64_t cols, void* out,
+                   int out_dtype, void* stream);
 
 }  // namespace sh

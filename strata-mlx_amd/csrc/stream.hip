@@ -86,13 +86,16 @@ template <typename XT> __device__ __forceinline__ void dot32h_lds(const float* w
 // Q3_K half a run (one scale each); 0: none
 template <int KIND> constexpr int stream_sum_group() { return KIND == Q2_0 ? 32 : KIND == Q3_K ? 16 : 0; }
 
-// idx: NULL (matrix m is the stack's m-th, its activations x[m]) or the expert of each pair m (a pair naming no
-// expert, outside [0, n_experts), gets zeros), its activations x[m / share] (one token a pair)
+// Matrix m is the stack's m-th with activations x[m]; or, for pairs (one token each, activations x[m / share]),
+// expert idx[m] of the stack (a pair naming no expert, outside [0, n_experts), gets zeros) or the buffer
+// experts[m]. An expert buffer need not start on 16 bytes: its first chunk is read from the 16 bytes holding its
+// first byte, inside the allocation it lies in (allocations start on 256 bytes).
 template <int KIND, typename XT, int TM>
 __global__ __launch_bounds__(SM_NT) void k_stream_mv(const uint8_t* __restrict__ blocks, StreamPlan S,
                                                      const XT* __restrict__ x, XT* __restrict__ out,
                                                      const uint8_t* __restrict__ tabs, const int32_t* __restrict__ idx,
-                                                     int n_experts, int share) {
+                                                     int n_experts, int share,
+                                                     const uint8_t* const* __restrict__ experts) {
   __shared__ u32x4 tab4[lds_tab_bytes(KIND) / 16];
   extern __shared__ u32x4 dyn[];
   uint8_t* tab = (uint8_t*)tab4;
@@ -125,9 +128,15 @@ __global__ __launch_bounds__(SM_NT) void k_stream_mv(const uint8_t* __restrict__
       s.valid = e >= 0 && e < n_experts;
       mat = s.valid ? e : 0;
     }
-    const int64_t off = mat * S.mat_bytes + (int64_t)s.r0 * S.rbytes;
-    s.a16 = blocks + (off & ~(int64_t)15);  // from the kernel argument: global loads
-    s.lead = (int)(off & 15);
+    if (experts) {
+      const uint8_t* a = experts[s.m] + (int64_t)s.r0 * S.rbytes;
+      s.a16 = (const uint8_t*)((uintptr_t)a & ~(uintptr_t)15);
+      s.lead = (int)(a - s.a16);
+    } else {
+      const int64_t off = mat * S.mat_bytes + (int64_t)s.r0 * S.rbytes;
+      s.a16 = blocks + (off & ~(int64_t)15);  // from the kernel argument: global loads
+      s.lead = (int)(off & 15);
+    }
     const int n = s.valid ? s.lead + s.nr * (int)S.rbytes : 0;
     s.nfull = n >> 4;
     s.ntail = n & 15;
@@ -277,7 +286,7 @@ __global__ __launch_bounds__(SM_NT) void k_stream_mv(const uint8_t* __restrict__
 static int stream_plan(int kind, int x_dtype, const void* blocks, const void* x, int64_t n_mats, int64_t rows,
                        int64_t cols, int64_t tokens, StreamPlan& S) {
   if (tokens < 1 || tokens > 8) return fail(E_UNSUPPORTED, "stream matvec: %lld tokens (1 to 8)", (long long)tokens);
-  if (((uintptr_t)blocks & 15) || ((uintptr_t)x & 15))
+  if (((uintptr_t)blocks & 15) || ((uintptr_t)x & 15))  // (blocks NULL: pairs bringing their own buffers)
     return fail(E_UNSUPPORTED, "stream matvec: blocks and activations must be 16-byte aligned");
   const int64_t runs = cols / 32, rb = row_bytes(kind, cols), xs = 32 * dtype_size(x_dtype) + 16;
   if (tokens * runs * xs > SM_X_MAX)
@@ -305,7 +314,8 @@ static int stream_plan(int kind, int x_dtype, const void* blocks, const void* x,
 
 template <int KIND, typename XT, int TM>
 static int launch_stream(const StreamPlan& S0, const uint8_t* blocks, const uint8_t* tabs, const XT* x, XT* out,
-                         hipStream_t stream, bool dry, const int32_t* idx, int n_experts, int share) {
+                         hipStream_t stream, bool dry, const int32_t* idx, int n_experts, int share,
+                         const uint8_t* const* experts) {
   StreamPlan S = S0;
   auto kern = k_stream_mv<KIND, XT, TM>;
   const size_t dyn_lds = (size_t)S.x_bytes + S.xsum_bytes + SM_TILE;
@@ -317,7 +327,7 @@ static int launch_stream(const StreamPlan& S0, const uint8_t* blocks, const uint
   S.per = (S.items + cap - 1) / cap;
   const int64_t grid = (S.items + S.per - 1) / S.per;
   hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(SM_NT), dyn_lds, stream, blocks, S, x, out, tabs, idx,
-                     n_experts, share);
+                     n_experts, share, experts);
   return check_launch("stream matvec");
 }
 
@@ -326,12 +336,12 @@ static int launch_stream(const StreamPlan& S0, const uint8_t* blocks, const uint
 // n_experts by x[m / share] (one token a pair).
 int stream_matvec(bool dry, int kind, const void* blocks, const void* tables, int64_t n_mats, int64_t rows,
                   int64_t cols, const void* x, int x_dtype, int64_t tokens, void* out, void* stream,
-                  const int32_t* idx, int64_t n_experts, int64_t share) {
+                  const int32_t* idx, int64_t n_experts, int64_t share, const void* const* experts) {
   int st = check_rows(kind, rows, cols, "stream matvec");
   if (st) return st;
-  if (!blocks || !x || (!out && !dry) || (needs_tables(kind) && !tables))
+  if ((!blocks && !experts) || !x || (!out && !dry) || (needs_tables(kind) && !tables))
     return fail(E_ARG, "stream matvec: null pointer");
-  if (idx && (tokens != 1 || share < 1 || n_experts < 0 || n_experts > (1ll << 31) - 1))
+  if ((idx || experts) && (tokens != 1 || share < 1 || n_experts < 0 || n_experts > (1ll << 31) - 1))
     return fail(E_UNSUPPORTED, "stream matvec: pairs of %lld tokens, share %lld", (long long)tokens,
                 (long long)share);
   StreamPlan S;
@@ -343,9 +353,133 @@ int stream_matvec(bool dry, int kind, const void* blocks, const void* tables, in
       using XT = std::remove_pointer_t<decltype(tp)>;
       if (tokens == 1)
         return launch_stream<K, XT, 1>(S, (const uint8_t*)blocks, (const uint8_t*)tables, (const XT*)x, (XT*)out,
-                                       (hipStream_t)stream, dry, idx, (int)n_experts, (int)share);
+                                       (hipStream_t)stream, dry, idx, (int)n_experts, (int)share,
+                                       (const uint8_t* const*)experts);
       return launch_stream<K, XT, 8>(S, (const uint8_t*)blocks, (const uint8_t*)tables, (const XT*)x, (XT*)out,
-                                     (hipStream_t)stream, dry, idx, (int)n_experts, (int)share);
+                                     (hipStream_t)stream, dry, idx, (int)n_experts, (int)share,
+                                       (const uint8_t* const*)experts);
+    });
+  });
+}
+
+// ---- dequantize: every weight of a tensor of rows as a float of OutT (strata_mlx/blocks.py:397-404), the same
+// memory path: an item's rows come in as 16-byte loads into LDS (the next item's into registers meanwhile), each
+// lane decodes runs of 32 from LDS (unpack32, the generic kernel's values) into an LDS output tile at a padded run
+// stride (16-byte writes in distinct banks), and the tile, contiguous in the output, leaves as consecutive
+// 16-byte stores of all 256 threads.
+
+constexpr int DQ_OUT = 32 * 1024;  // LDS bytes of an item's output rows (before padding)
+
+struct DequantPlan {
+  int64_t rows;  // rows of the whole tensor
+  int cols, runs, tile_rows, loads;
+  int64_t rbytes, items, per;
+  int in_bytes;  // LDS bytes of the input buffer
+};
+
+template <int KIND, typename OT>
+__global__ __launch_bounds__(SM_NT) void k_dequant_stream(const uint8_t* __restrict__ blocks, DequantPlan S,
+                                                          OT* __restrict__ out, const uint8_t* __restrict__ tabs) {
+  constexpr int RUN = 32 * (int)sizeof(OT), RSTR = RUN + 16, CPR = RUN / 16;  // a run's output bytes, stride, chunks
+  __shared__ u32x4 tab4[lds_tab_bytes(KIND) / 16];
+  extern __shared__ u32x4 dyn[];
+  uint8_t* tab = (uint8_t*)tab4;
+  uint8_t* tl = (uint8_t*)dyn;                // the item's bytes from the 16-byte chunk holding its first
+  uint8_t* ol = (uint8_t*)dyn + S.in_bytes;   // its output runs, RSTR bytes apart
+  const int tid = threadIdx.x;
+  const int64_t first = (int64_t)blockIdx.x * S.per, last = min(S.items, first + S.per);
+  if (first >= last) return;  // the whole block
+  stage_tables<KIND>(tab, tabs);
+  struct Span {
+    int64_t r0;
+    int nr, lead, nfull, ntail;
+    const uint8_t* a16;
+  };
+  auto span = [&](int64_t item) {
+    Span s;
+    s.r0 = item * S.tile_rows;
+    s.nr = (int)min((int64_t)S.tile_rows, S.rows - s.r0);
+    const int64_t off = s.r0 * S.rbytes;
+    s.a16 = blocks + (off & ~(int64_t)15);
+    s.lead = (int)(off & 15);
+    const int n = s.lead + s.nr * (int)S.rbytes;
+    s.nfull = n >> 4;
+    s.ntail = n & 15;
+    return s;
+  };
+  u32x4 stg[SM_LOADS];
+  uint32_t stail = 0;
+  auto issue = [&](const Span& s) {
+#pragma unroll
+    for (int j = 0; j < SM_LOADS; ++j) {
+      const int c = j * SM_NT + tid;
+      if (j < S.loads && c < s.nfull) stg[j] = *(const u32x4*)(s.a16 + 16 * c);
+    }
+    if (tid < s.ntail) stail = s.a16[16 * s.nfull + tid];
+  };
+  issue(span(first));
+  for (int64_t item = first; item < last; ++item) {
+    const Span s = span(item);
+    __syncthreads();  // every wave is done with the item before (its input and output tiles)
+#pragma unroll
+    for (int j = 0; j < SM_LOADS; ++j) {
+      const int c = j * SM_NT + tid;
+      if (j < S.loads && c < s.nfull) *(u32x4*)(tl + 16 * c) = stg[j];
+    }
+    if (tid < s.ntail) tl[16 * s.nfull + tid] = (uint8_t)stail;
+    if (item + 1 < last) issue(span(item + 1));
+    __syncthreads();
+    const int nruns = s.nr * S.runs;
+    for (int q = tid; q < nruns; q += SM_NT) {
+      const int r = q / S.runs, n = q - r * S.runs;
+      float w[32];
+      unpack32<KIND>(tl + s.lead + (int64_t)r * S.rbytes, n, w, tab);
+      OT o[32];
+#pragma unroll
+      for (int j = 0; j < 32; ++j) o[j] = from_f32<OT>(w[j]);
+#pragma unroll
+      for (int c = 0; c < CPR; ++c) *(u32x4*)(ol + q * RSTR + 16 * c) = ((const u32x4*)o)[c];
+    }
+    __syncthreads();
+    uint8_t* dst = (uint8_t*)(out + s.r0 * S.cols);
+    const int nch = nruns * CPR;
+    for (int c = tid; c < nch; c += SM_NT) {
+      const int q = c / CPR;
+      *(u32x4*)(dst + 16 * c) = *(const u32x4*)(ol + q * RSTR + 16 * (c - q * CPR));
+    }
+  }
+}
+
+// dequantize by the stream: E_UNSUPPORTED where it does not take the tensor (the caller takes the generic kernel)
+int dequant_stream(int kind, const void* blocks, const void* tables, int64_t rows, int64_t cols, void* out,
+                   int out_dtype, void* stream) {
+  if (((uintptr_t)blocks & 15) || ((uintptr_t)out & 15))
+    return fail(E_UNSUPPORTED, "dequantize stream: blocks and output must be 16-byte aligned");
+  const int64_t rb = row_bytes(kind, cols), ob = cols * dtype_size(out_dtype);
+  const int64_t fit = std::min<int64_t>((SM_TILE - 32) / rb, DQ_OUT / ob);
+  if (fit < 1) return fail(E_UNSUPPORTED, "dequantize stream: rows of %lld weights too long", (long long)cols);
+  DequantPlan S;
+  S.rows = rows, S.cols = (int)cols, S.runs = (int)(cols / 32), S.rbytes = rb;
+  S.tile_rows = (int)std::min(fit, std::max<int64_t>(1, rows / (2 * device_cus())));
+  S.items = (rows + S.tile_rows - 1) / S.tile_rows;
+  S.loads = (int)(((15 + (int64_t)S.tile_rows * rb) / 16 + SM_NT - 1) / SM_NT);
+  S.in_bytes = SM_TILE;
+  return with_kind(kind, [&](auto kc) {
+    constexpr int K = decltype(kc)::value;
+    return with_dtype(out_dtype, [&](auto* tp) {
+      using OT = std::remove_pointer_t<decltype(tp)>;
+      auto kern = k_dequant_stream<K, OT>;
+      const size_t dyn_lds = (size_t)SM_TILE + (size_t)S.tile_rows * S.runs * (32 * sizeof(OT) + 16);
+      const size_t lds = dyn_lds + static_lds(kern);
+      if (lds > LDS_BYTES) return fail(E_UNSUPPORTED, "dequantize stream: %zu bytes of LDS", lds);
+      const int64_t bpc = std::max<int64_t>(1, std::min<int64_t>(8, (int64_t)LDS_BYTES / (int64_t)lds));
+      const int64_t cap = (int64_t)device_cus() * bpc;
+      DequantPlan P = S;
+      P.per = (S.items + cap - 1) / cap;
+      const int64_t grid = (S.items + P.per - 1) / P.per;
+      hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(SM_NT), dyn_lds, (hipStream_t)stream, (const uint8_t*)blocks,
+                         P, (OT*)out, (const uint8_t*)tables);
+      return check_launch("dequantize");
     });
   });
 }

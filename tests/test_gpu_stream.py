@@ -40,14 +40,24 @@ def streamed(kind, dtype):
     return kind not in FACTORED and not (kind == "IQ3_S" and dtype != "float32")
 
 
+def off16(x):
+    """x's values in a buffer that does not start on 16 bytes (one element in): the stream does not take it."""
+    flat = torch.empty(x.numel() + 1, dtype=x.dtype, device=x.device)
+    out = flat[1:].view(x.shape)
+    out.copy_(x)
+    assert out.data_ptr() % 16
+    return out
+
+
 def generic(b, kind, shape, x, dev):
-    """The generic expert kernel (matvec_separate: a buffer a pair), pair t = matrix m's token t: the reference
-    bits of the stream."""
+    """The generic expert kernel (matvec_separate, a buffer a pair, activations off 16 bytes), pair t = matrix m's
+    token t: the reference bits of the stream."""
     n, rows, cols = shape
     tokens = x.shape[-2]
     mat = rows * SB.row_bytes(kind, cols)
     experts = [b[m * mat : (m + 1) * mat] for m in range(n) for _ in range(tokens)]
-    return SB.matvec_separate(experts, kind, rows, cols, x.reshape(-1, cols), 1).reshape(n, tokens, rows)
+    x1 = off16(x.reshape(-1, cols))
+    return SB.matvec_separate(experts, kind, rows, cols, x1, 1).reshape(n, tokens, rows)
 
 
 @pytest.mark.parametrize("kind", KINDS)
@@ -197,8 +207,31 @@ def test_expert_pairs_through_the_stream(kind, dtype, share, tables, dev):
         mat = R * SB.row_bytes(kind, C)
         ok = [p for p, e in enumerate(idx) if 0 <= e < E]
         sep = SB.matvec_separate([b[idx[p] * mat : (idx[p] + 1) * mat] for p in ok], kind, R, C,
-                                 torch.stack([x[p // share] for p in ok]).to(dev), 1).cpu()
+                                 off16(torch.stack([x[p // share] for p in ok]).to(dev)), 1).cpu()
         assert torch.equal(got[ok], sep)
+
+
+@pytest.mark.parametrize("kind", ["Q2_0", "IQ4_XS", "IQ2_XS"])
+@pytest.mark.parametrize("dtype", ["float32", "bfloat16"])
+def test_pairs_bringing_their_own_buffers(kind, dtype, tables, dev):
+    """matvec_separate (an expert buffer a pair, as the paged experts bring them): buffers starting anywhere in
+    their allocation (5 bytes in), the oracle's products; the generic kernel's bits for a codebook kind."""
+    R, C = 48, 768
+    raw, w = mats(kind, 3, R, C, 420, tables)
+    mat = R * SB.row_bytes(kind, C)
+    big = torch.zeros(3 * mat + 64, dtype=torch.uint8)
+    big[5 : 5 + 3 * mat] = torch.from_numpy(raw)
+    big = big.to(dev)
+    order = [2, 0, 2, 1]
+    experts = [big[5 + e * mat : 5 + (e + 1) * mat] for e in order]
+    rng = np.random.default_rng(421)
+    x, xv = act(rng, (len(order), C), dtype)
+    got = SB.matvec_separate(experts, kind, R, C, x.to(dev), 1).cpu()
+    for p, e in enumerate(order):
+        want = w[e].astype(np.float64) @ xv[p].astype(np.float64)
+        assert rel_err(got[p].float().numpy(), want) <= TOL[dtype]
+    if kind not in FACTORED:
+        assert torch.equal(got, SB.matvec_separate(experts, kind, R, C, off16(x.to(dev)), 1).cpu())
 
 
 @pytest.mark.parametrize("kind", ["Q2_0", "IQ2_S"])
@@ -227,3 +260,32 @@ def test_activations_off_16_bytes_take_the_generic_kernel(kind, tables, dev):
         assert torch.equal(pairs, SB.switch_matvec(b, kind, (E, R, C), idx, ok, 1).cpu())
     with pytest.raises(Exception, match="aligned"):
         SB.stack_matvec(b[:mat], kind, (1, R, C), off[None])
+
+
+@pytest.mark.parametrize("kind", KINDS)
+@pytest.mark.parametrize("dtype", ["float32", "bfloat16", "float16"])
+def test_dequantize_by_the_stream(kind, dtype, tables, dev):
+    """dequantize through the coalesced stream: the oracle's weights rounded once to the dtype, bit for bit, over
+    items of several rows, a last item of fewer, and rows whose bytes are not whole 16-byte chunks."""
+    cols = {"Q2_0": 2880, "IQ4_NL": 1120, "Q3_K": 2560}.get(kind, 1280)
+    raw, w = mats(kind, 3, 37, cols, 400, tables)
+    got = SB.dequantize(torch.from_numpy(raw).to(dev), kind, (3, 37, cols), TORCH[dtype]).cpu()
+    want = torch.from_numpy(w).to(TORCH[dtype])
+    assert got.shape == want.shape and torch.equal(got, want)
+    # an output that does not start on 16 bytes takes the generic kernel: the same values
+    flat = torch.empty(3 * 37 * cols + 1, dtype=TORCH[dtype], device=dev)
+    lib_out = flat[1:].view(3, 37, cols)
+    from strata_hip import _lib
+
+    blocks = torch.from_numpy(raw).to(dev)
+    _lib.call("sh_dequantize", SB._kind(kind), blocks.data_ptr(), SB._tabs(kind, lib_out.device), 3, 37, cols,
+              lib_out.data_ptr(), _lib.dtype_code(TORCH[dtype]), _lib.stream_of(lib_out))
+    assert torch.equal(lib_out.cpu(), want)
+
+
+def test_dequantize_many_items_a_block(tables, dev):
+    """A tensor of 9,000 rows: items of 5 rows, each block several items (the next item's loads in flight while
+    one is decoded)."""
+    raw, w = mats("Q2_0", 3, 3000, 2880, 410, tables)
+    got = SB.dequantize(torch.from_numpy(raw).to(dev), "Q2_0", (3, 3000, 2880), torch.bfloat16).cpu()
+    assert torch.equal(got, torch.from_numpy(w).to(torch.bfloat16))
