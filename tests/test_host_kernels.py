@@ -27,7 +27,7 @@ SELECTION = [
                         "or whole_blocks"),
     ("test_gpu_tiles.py", "not 4096 and not skewed"),
     ("test_gpu_dropin.py", "not reference_models_shape and not install_routers"),
-    ("test_gpu_stream.py", "not benchmark_shape"),
+    ("test_gpu_stream.py", "not benchmark_shape and not many_items"),
 ]
 
 
