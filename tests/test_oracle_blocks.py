@@ -108,3 +108,17 @@ def test_row_bytes_rejects_partial_blocks():
     assert OB.row_bytes("IQ3_S", 2048) == 880 and OB.row_bytes("Q2_0", 2048) == 576
     with pytest.raises(ValueError):
         OB.row_bytes("IQ3_S", 640)
+
+
+def test_ksigns_is_ggmls_published_table():
+    """The sign table the IQ2_XS / IQ2_XXS / IQ3_XXS kinds read: the first 32 of the 128 entries of ggml's
+    ksigns_iq2xs (ggml-common.h) as published, and every entry seven stored sign bits with an eighth making the
+    count of set bits even (the property the decoders rely on: a group's signs are 7 bits in the block)."""
+    from strata_hip import tables as T
+
+    k = T.even_parity_signs()
+    published = [0, 129, 130, 3, 132, 5, 6, 135, 136, 9, 10, 139, 12, 141, 142, 15,
+                 144, 17, 18, 147, 20, 149, 150, 23, 24, 153, 154, 27, 156, 29, 30, 159]
+    assert k.dtype == np.uint8 and k.shape == (128,)
+    assert list(k[:32]) == published
+    assert all((int(v) & 127) == i and bin(int(v)).count("1") % 2 == 0 for i, v in enumerate(k))
